@@ -1,0 +1,148 @@
+/*
+ * mq4.h -- C ABI of the MI355X (gfx950) MLX-affine Q4 matrix-product library.
+ *
+ * Data formats are MLX's affine 4-bit layout, byte for byte, so tensors
+ * produced by mx::quantize load unchanged:
+ *   w      bf16 [N, K] row-major (uint16_t bit patterns)
+ *   wq     uint32 [N, K/8]; nibble p (bits 4p..4p+3) of word j holds element
+ *          8j+p of the row (low nibble first)
+ *   scales bf16 [N, K/64], biases bf16 [N, K/64]; element k of row n
+ *          dequantizes to scales[n, k/64] * q + biases[n, k/64]
+ *   x      bf16 [M, K] row-major; y bf16 [M, N] row-major
+ * Only group_size 64 and bits 4 are implemented; other values return
+ * MQ4_ERR_UNSUPPORTED.  K must be a positive multiple of 64.
+ *
+ * All pointers are device pointers (hipMalloc'd or equivalent) and `stream`
+ * is a hipStream_t (NULL = the default stream).  Every call is asynchronous
+ * and stream-ordered: it validates its arguments on the host, enqueues its
+ * kernels and returns; no call synchronizes the device.  Errors are returned
+ * as negative status codes with a message in mq4_last_error() (per host
+ * thread); no C++ exception crosses this boundary.
+ *
+ * Reference seams replaced (paths relative to the marlin-mlx repository):
+ *   mq4_quantize         mx::quantize(w, 64, 4) in quantize_weight
+ *                        (src/model/weights.cpp:45-56) and the lm_head load
+ *                        (src/model/weights.cpp:180-194)
+ *   mq4_qmm              mx::quantized_matmul(x, w, s, b, true, 64, 4) in
+ *                        qmatmul (src/model/marlin.cpp:18-25) and
+ *                        MarlinModel::lm_head (src/model/marlin.cpp:161-169)
+ *   mq4_mlp_gate_up_silu swiglu(qmatmul(x, gate), qmatmul(x, up))
+ *                        (src/model/marlin.cpp:27-33)
+ *   mq4_swiglu_bf16      swiglu(gate, up) (src/model/marlin.cpp:27-29)
+ *   mq4_qmm_residual     hidden + qmatmul(h, down)
+ *                        (src/model/marlin.cpp:34, 142)
+ *   mq4_lm_head_argmax   sample_token(lm_head(h)) with temperature <= 0
+ *                        (src/model/marlin.cpp:161-169,
+ *                        src/sampling/sampler.cpp:9-16)
+ *   mq4_argmax_bf16      mx::argmax(last_logits, -1)
+ *                        (src/sampling/sampler.cpp:15)
+ */
+#ifndef MQ4_H
+#define MQ4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum mq4_status {
+    MQ4_OK = 0,
+    MQ4_ERR_INVALID_ARG = -1,   /* null pointer, non-positive or inconsistent shape */
+    MQ4_ERR_UNSUPPORTED = -2,   /* group_size != 64, bits != 4, transpose == 0, K too large */
+    MQ4_ERR_ALIGNMENT = -3,     /* pointer not aligned as the call requires */
+    MQ4_ERR_HIP = -4,           /* a HIP runtime call or kernel launch failed */
+    MQ4_ERR_WORKSPACE = -5      /* workspace missing or too small */
+};
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* mq4_last_error(void);
+
+/* Library version, major*10000 + minor*100 + patch. */
+int mq4_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* Quantize / pack.  Replaces mx::quantize(w, group_size=64, bits=4)
+ * (src/model/weights.cpp:46 and :183).  Bit-exact MLX affine quantization
+ * computed in float32: per group of 64, scale = +-max((max-min)/15, 1e-7)
+ * (negative unless |min| > |max|), edge = the larger-magnitude extreme,
+ * q0 = rint(edge/scale), scale = edge/q0 and bias = edge when q0 != 0 (else
+ * bias = 0), q = clip(rint((w - bias)/scale), 0, 15) with round-half-even.
+ * w must be 16-byte aligned, wq 4-byte, scales/biases 2-byte. */
+int mq4_quantize(const uint16_t* w, int64_t N, int64_t K, int group_size, int bits,
+                 uint32_t* wq, uint16_t* scales, uint16_t* biases, void* stream);
+
+/* Dequantize: out = scales*q + biases, rounded once (round-to-nearest-even)
+ * to bf16 (out_f32 == 0, out is uint16_t*) or stored exactly as float
+ * (out_f32 != 0, out is float*).  Test and inspection helper. */
+int mq4_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                   int64_t N, int64_t K, int group_size, int bits, void* out, int out_f32,
+                   void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* y[M, N] = x[M, K] @ dequant(wq, scales, biases)^T, fp32 accumulation,
+ * one bf16 rounding of each output.  Replaces
+ * mx::quantized_matmul(x, w, scales, biases, transpose=true, 64, 4)
+ * (src/model/marlin.cpp:20-22 and :164-166).  transpose must be 1 (the only
+ * form the reference uses).  x and wq must be 16-byte aligned. */
+int mq4_qmm(const uint16_t* x, int64_t M, int64_t K,
+            const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int64_t N,
+            int transpose, int group_size, int bits, uint16_t* y, void* stream);
+
+/* y = bf16(residual + bf16(x @ W^T)): the down projection with the residual
+ * add that follows it (src/model/marlin.cpp:34 and :142).  residual [M, N]
+ * may alias y (in-place update of the hidden state). */
+int mq4_qmm_residual(const uint16_t* x, int64_t M, int64_t K,
+                     const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                     int64_t N, const uint16_t* residual, uint16_t* y, void* stream);
+
+/* h[M, N] = swiglu(x @ Wg^T, x @ Wu^T) with MLX's bf16 op order
+ * (src/model/marlin.cpp:27-33): g = bf16(x@Wg^T), u = bf16(x@Wu^T),
+ * h = bf16(bf16(bf16(sigmoid(g)) * g) * u).  gate and up are both [N, K]. */
+int mq4_mlp_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
+                         const uint32_t* gate_wq, const uint16_t* gate_scales,
+                         const uint16_t* gate_biases,
+                         const uint32_t* up_wq, const uint16_t* up_scales,
+                         const uint16_t* up_biases,
+                         int64_t N, uint16_t* h, void* stream);
+
+/* out[i] = bf16(bf16(bf16(sigmoid(gate[i])) * gate[i]) * up[i]): the
+ * unfused swiglu (src/model/marlin.cpp:27-29) over n bf16 elements. */
+int mq4_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* out,
+                    void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Greedy lm_head: logits = bf16(h @ W^T) for each of the M rows and
+ * idx[m] = argmax over the N bf16 logits of row m, the lowest index winning
+ * ties (mx::argmax semantics; src/sampling/sampler.cpp:15).  logits (may be
+ * NULL) receives the [M, N] bf16 logits.  workspace is device memory of at
+ * least mq4_lm_head_argmax_workspace_size(M, N) bytes, 8-byte aligned; it
+ * holds per-block partial results and may be reused by any later call on the
+ * same stream. */
+size_t mq4_lm_head_argmax_workspace_size(int64_t M, int64_t N);
+int mq4_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K,
+                       const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                       int64_t N, uint32_t* idx, uint16_t* logits,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* idx[m] = argmax of row m of bf16 logits [M, N] (lowest index wins ties,
+ * NaN never wins over a number).  Same workspace rule as above with
+ * mq4_argmax_workspace_size. */
+size_t mq4_argmax_workspace_size(int64_t M, int64_t N);
+int mq4_argmax_bf16(const uint16_t* logits, int64_t M, int64_t N, uint32_t* idx,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Synthetic-input generator (bench and test inputs, not a reference seam):
+ * out[i] = bf16(mu + sigma * z_{offset+i}) where z is the standard-normal
+ * stream (SplitMix64 counter stream with state seed ^ stream_id, Box-Muller
+ * in fp64, one round-to-nearest-even step from fp64 to bf16). */
+int mq4_fill_normal_bf16(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream_id,
+                         double mu, double sigma, int64_t offset, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MQ4_H */

@@ -1,0 +1,344 @@
+"""marlin-mlx_amd: MI355X-native MLX-affine Q4 matrix products for marlin-mlx.
+
+Python mirror of the reference's interface for the quantized path, over the
+C ABI of libmq4.so (include/mq4.h).  torch provides device memory and the
+current HIP stream only; every byte of arithmetic runs in the gfx950 kernels of
+libmq4.so.  If that library is missing the import fails (there is no fallback).
+
+Reference seams mirrored (paths relative to the marlin-mlx repository):
+  QuantizedTensor        src/core/types.h:75-82
+  quantize_weight        src/model/weights.cpp:45-56 (and :180-194 for lm_head)
+  qmatmul                src/model/marlin.cpp:18-25
+  swiglu                 src/model/marlin.cpp:27-29
+  mlp_forward            src/model/marlin.cpp:31-35
+  lm_head                src/model/marlin.cpp:161-169
+  sample_token (greedy)  src/sampling/sampler.cpp:9-16
+and the MLX ops they call: quantize, dequantize, quantized_matmul, argmax.
+
+Tensor conventions: bf16 tensors are torch.bfloat16; packed weights are
+torch.int32 holding the uint32 words of MLX's layout; indices are torch.int32.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+__all__ = [
+    "MQ4Error", "library_path", "lib", "QuantizedTensor", "MLPWeights",
+    "quantize", "dequantize", "quantized_matmul", "argmax", "swiglu",
+    "quantize_weight", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
+    "lm_head", "lm_head_argmax", "sample_token", "fill_normal_bf16",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libmq4.so")
+_lib = None
+
+GROUP_SIZE = 64
+BITS = 4
+
+# Stream ids of the synthetic-input generator (SplitMix64 seed ^ stream id).
+SEED = 0x4D41524C  # "MARL"
+
+
+def stream_id_layer(layer: int, proj: int) -> int:
+    """gate=0, up=1, down=2 of layer `layer`."""
+    return 1000 + 3 * layer + proj
+
+
+STREAM_LM_HEAD = 2000
+STREAM_NORM_WEIGHT = 2001
+
+
+def stream_id_decode_row(m: int) -> int:
+    return 3000 + m
+
+
+STREAM_PREFILL = 4000
+
+
+class MQ4Error(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"libmq4 error {code}: {message}")
+        self.code = code
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def lib():
+    """The loaded libmq4.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        raise RuntimeError(
+            f"{_LIB_PATH} is missing: build it with `python marlin-mlx_amd/build.py` "
+            "(there is no non-HIP fallback)")
+    L = ctypes.CDLL(_LIB_PATH)
+    P, I64, I, SZ, U64, D = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t,
+                             ctypes.c_uint64, ctypes.c_double)
+    sig = {
+        "mq4_last_error": ([], ctypes.c_char_p),
+        "mq4_version": ([], I),
+        "mq4_quantize": ([P, I64, I64, I, I, P, P, P, P], I),
+        "mq4_dequantize": ([P, P, P, I64, I64, I, I, P, I, P], I),
+        "mq4_qmm": ([P, I64, I64, P, P, P, I64, I, I, I, P, P], I),
+        "mq4_qmm_residual": ([P, I64, I64, P, P, P, I64, P, P, P], I),
+        "mq4_mlp_gate_up_silu": ([P, I64, I64, P, P, P, P, P, P, I64, P, P], I),
+        "mq4_swiglu_bf16": ([P, P, I64, P, P], I),
+        "mq4_lm_head_argmax_workspace_size": ([I64, I64], SZ),
+        "mq4_lm_head_argmax": ([P, I64, I64, P, P, P, I64, P, P, P, SZ, P], I),
+        "mq4_argmax_workspace_size": ([I64, I64], SZ),
+        "mq4_argmax_bf16": ([P, I64, I64, P, P, SZ, P], I),
+        "mq4_fill_normal_bf16": ([P, I64, U64, U64, D, D, I64, P], I),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise MQ4Error(rc, lib().mq4_last_error().decode())
+
+
+def _stream(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _need(t: torch.Tensor, dtype, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    return t.contiguous()
+
+
+# ----------------------------------------------------------------- ops ---
+
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4):
+    """mx::quantize(w, group_size, bits) for bf16 w [..., K]: returns
+    (wq int32 [..., K/8], scales bf16 [..., K/64], biases bf16 [..., K/64])."""
+    w = _need(w, torch.bfloat16, "w")
+    K = w.shape[-1]
+    N = w.numel() // K if K else 0
+    lead = w.shape[:-1]
+    wq = torch.empty((*lead, K // 8), dtype=torch.int32, device=w.device)
+    s = torch.empty((*lead, K // max(group_size, 1)), dtype=torch.bfloat16, device=w.device)
+    b = torch.empty_like(s)
+    _check(lib().mq4_quantize(_ptr(w), N, K, group_size, bits, _ptr(wq), _ptr(s), _ptr(b),
+                              _stream(w.device)))
+    return wq, s, b
+
+
+def dequantize(wq: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               group_size: int = 64, bits: int = 4, dtype=torch.bfloat16) -> torch.Tensor:
+    wq = _need(wq, torch.int32, "wq")
+    scales = _need(scales, torch.bfloat16, "scales")
+    biases = _need(biases, torch.bfloat16, "biases")
+    K = wq.shape[-1] * 8
+    N = wq.numel() * 8 // K
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("dequantize: dtype must be bfloat16 or float32")
+    out = torch.empty((*wq.shape[:-1], K), dtype=dtype, device=wq.device)
+    _check(lib().mq4_dequantize(_ptr(wq), _ptr(scales), _ptr(biases), N, K, group_size, bits,
+                                _ptr(out), int(dtype == torch.float32), _stream(wq.device)))
+    return out
+
+
+def _mk(x: torch.Tensor, N: int):
+    K = x.shape[-1]
+    M = x.numel() // K
+    y = torch.empty((*x.shape[:-1], N), dtype=torch.bfloat16, device=x.device)
+    return M, K, y
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                     transpose: bool = True, group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """mx::quantized_matmul(x, w, scales, biases, transpose, group_size, bits):
+    x bf16 [..., K] @ dequant(w [N, K/8])^T -> bf16 [..., N]."""
+    x = _need(x, torch.bfloat16, "x")
+    w = _need(w, torch.int32, "w")
+    scales = _need(scales, torch.bfloat16, "scales")
+    biases = _need(biases, torch.bfloat16, "biases")
+    N = w.shape[0]
+    M, K, y = _mk(x, N)
+    _check(lib().mq4_qmm(_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N, int(transpose),
+                         group_size, bits, _ptr(y), _stream(x.device)))
+    return y
+
+
+def argmax(logits: torch.Tensor, axis: int = -1) -> torch.Tensor:
+    """mx::argmax(logits, -1) over bf16 logits: lowest index wins ties."""
+    if axis not in (-1, logits.dim() - 1):
+        raise NotImplementedError("argmax: only the last axis is supported")
+    logits = _need(logits, torch.bfloat16, "logits")
+    N = logits.shape[-1]
+    M = logits.numel() // N
+    idx = torch.empty(logits.shape[:-1], dtype=torch.int32, device=logits.device)
+    L = lib()
+    ws_bytes = L.mq4_argmax_workspace_size(M, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=logits.device)
+    _check(L.mq4_argmax_bf16(_ptr(logits), M, N, _ptr(idx), _ptr(ws), ws_bytes,
+                             _stream(logits.device)))
+    return idx
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """(sigmoid(gate) * gate) * up with a bf16 result after each op
+    (src/model/marlin.cpp:27-29)."""
+    gate = _need(gate, torch.bfloat16, "gate")
+    up = _need(up, torch.bfloat16, "up")
+    if gate.shape != up.shape:
+        raise ValueError("swiglu: gate and up shapes differ")
+    out = torch.empty_like(gate)
+    _check(lib().mq4_swiglu_bf16(_ptr(gate), _ptr(up), gate.numel(), _ptr(out),
+                                 _stream(gate.device)))
+    return out
+
+
+# ------------------------------------------------- reference interface ---
+
+@dataclass
+class QuantizedTensor:
+    """src/core/types.h:75-82: weight (packed uint32 words as int32), scales,
+    biases (bf16), group_size=64, bits=4, quantized."""
+    weight: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    group_size: int = 64
+    bits: int = 4
+    quantized: bool = True
+
+    @property
+    def out_features(self) -> int:
+        return self.weight.shape[0]
+
+    @property
+    def in_features(self) -> int:
+        return self.weight.shape[-1] * 32 // self.bits if self.quantized else self.weight.shape[-1]
+
+
+@dataclass
+class MLPWeights:
+    """src/model/marlin.h:17-21."""
+    gate_proj: QuantizedTensor
+    up_proj: QuantizedTensor
+    down_proj: QuantizedTensor
+
+
+def quantize_weight(w: torch.Tensor, bits: int = 4, group_size: int = 64) -> QuantizedTensor:
+    """src/model/weights.cpp:45-56: quantize a bf16 [N, K] weight."""
+    wq, s, b = quantize(w, group_size, bits)
+    return QuantizedTensor(wq, s, b, group_size, bits, True)
+
+
+def _require_quantized(w: QuantizedTensor, fn: str) -> None:
+    if not w.quantized:
+        raise NotImplementedError(
+            f"{fn}: unquantized (bf16 dense) weights are outside this library's path")
+
+
+def qmatmul(x: torch.Tensor, w: QuantizedTensor) -> torch.Tensor:
+    """src/model/marlin.cpp:18-25 (quantized branch)."""
+    _require_quantized(w, "qmatmul")
+    return quantized_matmul(x, w.weight, w.scales, w.biases, True, w.group_size, w.bits)
+
+
+def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor) -> torch.Tensor:
+    """swiglu(qmatmul(x, gate), qmatmul(x, up)) in one pass over both weights."""
+    _require_quantized(gate, "mlp_gate_up_silu")
+    _require_quantized(up, "mlp_gate_up_silu")
+    x = _need(x, torch.bfloat16, "x")
+    N = gate.out_features
+    if up.out_features != N:
+        raise ValueError("mlp_gate_up_silu: gate and up must have the same shape")
+    M, K, h = _mk(x, N)
+    _check(lib().mq4_mlp_gate_up_silu(
+        _ptr(x), M, K, _ptr(gate.weight), _ptr(gate.scales), _ptr(gate.biases),
+        _ptr(up.weight), _ptr(up.scales), _ptr(up.biases), N, _ptr(h), _stream(x.device)))
+    return h
+
+
+def qmatmul_residual(x: torch.Tensor, w: QuantizedTensor, residual: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """residual + qmatmul(x, w) with bf16 rounding of both (src/model/marlin.cpp:142);
+    out may be residual itself (in-place)."""
+    _require_quantized(w, "qmatmul_residual")
+    x = _need(x, torch.bfloat16, "x")
+    residual = _need(residual, torch.bfloat16, "residual")
+    N = w.out_features
+    K = x.shape[-1]
+    M = x.numel() // K
+    if residual.numel() != M * N:
+        raise ValueError("qmatmul_residual: residual shape mismatch")
+    y = out if out is not None else torch.empty_like(residual)
+    _check(lib().mq4_qmm_residual(_ptr(x), M, K, _ptr(w.weight), _ptr(w.scales), _ptr(w.biases), N,
+                                  _ptr(residual), _ptr(y), _stream(x.device)))
+    return y
+
+
+def mlp_forward(x: torch.Tensor, w: MLPWeights, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """src/model/marlin.cpp:31-35 (down(swiglu(gate x, up x))); with `residual`
+    also the add of src/model/marlin.cpp:142."""
+    h = mlp_gate_up_silu(x, w.gate_proj, w.up_proj)
+    if residual is None:
+        return qmatmul(h, w.down_proj)
+    return qmatmul_residual(h, w.down_proj, residual)
+
+
+def lm_head(hidden: torch.Tensor, w: QuantizedTensor) -> torch.Tensor:
+    """src/model/marlin.cpp:161-169 (quantized branch): bf16 logits."""
+    return qmatmul(hidden, w)
+
+
+def lm_head_argmax(hidden: torch.Tensor, w: QuantizedTensor, return_logits: bool = False):
+    """Greedy next token of every row of `hidden`: argmax of the bf16 logits,
+    fused with the lm_head product (marlin.cpp:161-169 + sampler.cpp:14-16)."""
+    _require_quantized(w, "lm_head_argmax")
+    hidden = _need(hidden, torch.bfloat16, "hidden")
+    N = w.out_features
+    K = hidden.shape[-1]
+    M = hidden.numel() // K
+    idx = torch.empty(hidden.shape[:-1], dtype=torch.int32, device=hidden.device)
+    logits = (torch.empty((*hidden.shape[:-1], N), dtype=torch.bfloat16, device=hidden.device)
+              if return_logits else None)
+    L = lib()
+    ws_bytes = L.mq4_lm_head_argmax_workspace_size(M, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden.device)
+    _check(L.mq4_lm_head_argmax(_ptr(hidden), M, K, _ptr(w.weight), _ptr(w.scales), _ptr(w.biases),
+                                N, _ptr(idx), _ptr(logits), _ptr(ws), ws_bytes,
+                                _stream(hidden.device)))
+    return (idx, logits) if return_logits else idx
+
+
+def sample_token(logits: torch.Tensor, temperature: float = 0.0) -> torch.Tensor:
+    """src/sampling/sampler.cpp:9-16: the last row of [1, S, V] logits, greedy.
+    Stochastic sampling (temperature > 0) is outside this library's path."""
+    if temperature > 0.0:
+        raise NotImplementedError("sample_token: only greedy (temperature <= 0) sampling is provided")
+    last = logits[:, -1, :] if logits.dim() == 3 else logits
+    return argmax(last.contiguous(), -1)
+
+
+def fill_normal_bf16(shape, stream_id: int, mu: float = 0.0, sigma: float = 1.0,
+                     device="cuda", seed: int = SEED, offset: int = 0) -> torch.Tensor:
+    """Synthetic bf16 N(mu, sigma) tensor from the counter-based generator."""
+    out = torch.empty(shape, dtype=torch.bfloat16, device=device)
+    _check(lib().mq4_fill_normal_bf16(_ptr(out), out.numel(), seed, stream_id, mu, sigma, offset,
+                                      _stream(out.device)))
+    return out

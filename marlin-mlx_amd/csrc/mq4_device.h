@@ -1,0 +1,118 @@
+// Device-side helpers shared by the gfx950 kernels of libmq4.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mq4 {
+
+constexpr int kWave = 64;     // CDNA wavefront width
+constexpr int kGroup = 64;    // MLX affine group size along K
+constexpr int kSlice = 32;    // K elements per 16-byte packed slice (4 words)
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (non-temporal hint: data read once).
+__device__ __forceinline__ uint4 load_nt_u4(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+    return __uint_as_float(h << 16);
+}
+
+// float -> bf16 bits, round to nearest even; NaN becomes a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// Round to bf16 and back (the value a bf16 tensor would hold).
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// 2-way bf16 dot product with fp32 accumulate: a.lo*b.lo + a.hi*b.hi + c.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Nibbles p and p+4 of a packed word as the bf16 pair (128 + q_p, 128 + q_{p+4}):
+// 0x4300 is bf16 128.0 and its 7 mantissa bits hold q exactly.
+template <int P>
+__device__ __forceinline__ uint32_t nib_pair_bf16(uint32_t word) {
+    return ((word >> (4 * P)) & 0x000F000Fu) | 0x43004300u;
+}
+
+// Monotone 16-bit key of a bf16 value for max-selection: larger value ->
+// larger key; -0 maps like +0 and NaN maps to 0 (below every number).
+__device__ __forceinline__ uint32_t bf16_order_key(uint32_t h) {
+    h &= 0xffffu;
+    if ((h & 0x7fffu) > 0x7f80u) return 0u;     // NaN
+    if (h == 0x8000u) h = 0u;                   // -0 -> +0
+    return (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+}
+
+// 64-bit argmax key: value key in the high word, ~index in the low word so
+// that among equal values the lowest index is the maximum.
+__device__ __forceinline__ uint64_t argmax_key(uint32_t bf16_bits, uint32_t index) {
+    return ((uint64_t)bf16_order_key(bf16_bits) << 32) | (uint64_t)(0xffffffffu - index);
+}
+__device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
+    return 0xffffffffu - (uint32_t)(key & 0xffffffffu);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    uint32_t lo = __shfl_xor((uint32_t)v, m);
+    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        uint64_t o = shfl_xor_u64(v, m);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Reduce V per-lane values (V a power of two, 1..64) over the 64 lanes of a
+// wave by recursive halving: at each xor step a lane keeps one half of its
+// values and adds the partner's copy of that half.  Afterwards v[0] of lane l
+// holds the wave-wide sum of value index (l >> (6 - log2 V)); the lanes with
+// (l & (64/V - 1)) == 0 are the designated holders of each index.
+template <int V>
+__device__ __forceinline__ float wave_multi_reduce(float (&v)[V], int lane) {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+    int count = V;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        if (count > 1) {
+            const bool upper = (lane & off) != 0;
+            const int h = count >> 1;
+#pragma unroll
+            for (int i = 0; i < V / 2; ++i) {
+                if (i < h) {
+                    float send = upper ? v[i] : v[i + h];
+                    float keep = upper ? v[i + h] : v[i];
+                    v[i] = keep + __shfl_xor(send, off);
+                }
+            }
+            count = h;
+        } else {
+            v[0] += __shfl_xor(v[0], off);
+        }
+    }
+    return v[0];
+}
+
+template <int V>
+__device__ __forceinline__ constexpr int log2_const() {
+    return V <= 1 ? 0 : 1 + log2_const<V / 2>();
+}
+
+}  // namespace mq4

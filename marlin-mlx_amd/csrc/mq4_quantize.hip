@@ -1,0 +1,228 @@
+// MLX-affine Q4 (group 64) quantize/pack, dequantize and the synthetic
+// normal generator, for gfx950.
+//
+// quantize follows mx::quantize(w, 64, 4) as called from quantize_weight
+// (src/model/weights.cpp:45-56) and the lm_head load
+// (src/model/weights.cpp:180-194); the arithmetic is MLX v0.25.2's CPU affine
+// quantize (mlx/backend/cpu/quantized.cpp), restated here in float32 with
+// correctly rounded division and round-half-even rint, so that packed words,
+// scales and biases are bit-identical.
+//
+// Layout observation that shapes the kernel: with K % 64 == 0 the groups of a
+// row-major [N, K] matrix are consecutive 64-element (128-byte) runs, and the
+// packed words, scales and biases of group g sit at wq[8g..8g+7], scales[g],
+// biases[g].  So the whole matrix is one flat stream of groups and the kernel
+// never needs N or K: each lane reads 16 bytes (8 bf16) and writes one packed
+// word, eight lanes form a group, and a wave covers 8 groups = 1 KiB of input
+// with fully coalesced 16-byte loads and 256-byte word stores.
+#include "mq4_device.h"
+#include "mq4_host.h"
+
+namespace mq4 {
+
+__device__ __forceinline__ float mlx_max(float a, float b) { return (a < b) ? b : a; }
+__device__ __forceinline__ float mlx_min(float a, float b) { return (b < a) ? b : a; }
+
+__global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w,
+                                                           int64_t n_words,
+                                                           uint32_t* __restrict__ wq,
+                                                           uint16_t* __restrict__ scales,
+                                                           uint16_t* __restrict__ biases) {
+#pragma clang fp contract(off)
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    // The loop bound is block-uniform so the cross-lane reductions below run
+    // with every lane of the wave active.
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < n_words; base += stride) {
+        const int64_t i = base + threadIdx.x;
+        const bool live = i < n_words;   // uniform within each 8-lane group
+        uint4 v = live ? load_nt_u4(w + i) : make_uint4(0u, 0u, 0u, 0u);
+        float f[8];
+        f[0] = bf16_to_f32(v.x & 0xffffu); f[1] = bf16_to_f32(v.x >> 16);
+        f[2] = bf16_to_f32(v.y & 0xffffu); f[3] = bf16_to_f32(v.y >> 16);
+        f[4] = bf16_to_f32(v.z & 0xffffu); f[5] = bf16_to_f32(v.z >> 16);
+        f[6] = bf16_to_f32(v.w & 0xffffu); f[7] = bf16_to_f32(v.w >> 16);
+
+        // Group extremes; NaN never wins (IEEE maxNum/minNum), matching MLX's
+        // std::max/std::min scan from -inf/+inf.
+        float mx = -__builtin_inff(), mn = __builtin_inff();
+#pragma unroll
+        for (int p = 0; p < 8; ++p) { mx = fmaxf(mx, f[p]); mn = fminf(mn, f[p]); }
+#pragma unroll
+        for (int m = 1; m < 8; m <<= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, m));
+            mn = fminf(mn, __shfl_xor(mn, m));
+        }
+
+        const float n_bins = 15.0f;
+        const float eps = 1e-7f;
+        float scale = mlx_max((mx - mn) / n_bins, eps);
+        const bool side = fabsf(mn) > fabsf(mx);
+        scale = side ? scale : -scale;
+        const float edge = side ? mn : mx;
+        const float q0 = __builtin_rintf(edge / scale);
+        float bias = 0.0f;
+        if (q0 != 0.0f) {
+            scale = edge / q0;
+            bias = edge;
+        }
+
+        uint32_t word = 0;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            float q = __builtin_rintf((f[p] - bias) / scale);
+            q = mlx_min(mlx_max(q, 0.0f), n_bins);
+            const uint32_t qi = (q == q) ? (uint32_t)q : 0u;   // NaN -> 0
+            word |= qi << (4 * p);
+        }
+        if (live) {
+            wq[i] = word;
+            if ((threadIdx.x & 7) == 0) {
+                scales[i >> 3] = (uint16_t)f32_to_bf16(scale);
+                biases[i >> 3] = (uint16_t)f32_to_bf16(bias);
+            }
+        }
+    }
+}
+
+// One packed word per lane: 8 outputs = scale * q + bias (q * scale is exact
+// for a bf16 scale and a 4-bit q; the add rounds once in float).
+template <bool F32>
+__global__ __launch_bounds__(256) void dequantize_g64_kernel(const uint32_t* __restrict__ wq,
+                                                             const uint16_t* __restrict__ scales,
+                                                             const uint16_t* __restrict__ biases,
+                                                             int64_t n_words, void* __restrict__ out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words; i += stride) {
+        const uint32_t word = wq[i];
+        const float s = bf16_to_f32(scales[i >> 3]);
+        const float b = bf16_to_f32(biases[i >> 3]);
+        float o[8];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) o[p] = __fmaf_rn(s, (float)((word >> (4 * p)) & 0xfu), b);
+        if (F32) {
+            float4* dst = reinterpret_cast<float4*>(out) + 2 * i;
+            dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+            dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+        } else {
+            uint4 r;
+            r.x = f32_to_bf16(o[0]) | (f32_to_bf16(o[1]) << 16);
+            r.y = f32_to_bf16(o[2]) | (f32_to_bf16(o[3]) << 16);
+            r.z = f32_to_bf16(o[4]) | (f32_to_bf16(o[5]) << 16);
+            r.w = f32_to_bf16(o[6]) | (f32_to_bf16(o[7]) << 16);
+            reinterpret_cast<uint4*>(out)[i] = r;
+        }
+    }
+}
+
+// ------------------------------------------------------------ generator ---
+
+__device__ __forceinline__ uint64_t sm64_mix(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// double -> bf16 bits in one round-to-nearest-even step (normal range; the
+// tiny or non-finite cases go through float).
+__device__ __forceinline__ uint32_t f64_to_bf16(double d) {
+    const uint64_t u = (uint64_t)__double_as_longlong(d);
+    const uint64_t sign = u >> 63;
+    const int e = (int)((u >> 52) & 0x7ff);
+    const int eb = e - 1023 + 127;
+    if (e == 0x7ff || eb <= 0) return f32_to_bf16((float)d);
+    uint64_t v = ((uint64_t)eb << 52) | (u & ((1ull << 52) - 1));
+    v += (1ull << 44) - 1 + ((v >> 45) & 1ull);
+    v >>= 45;
+    if (v >= 0xff80ull) v = 0x7f80ull;
+    return (uint32_t)((sign << 15) | v);
+}
+
+// Element pair j of stream state s0: SplitMix64 outputs 2j and 2j+1 feed one
+// Box-Muller draw (cos -> element 2j, sin -> element 2j+1).
+__global__ __launch_bounds__(256) void fill_normal_bf16_kernel(uint16_t* __restrict__ out, int64_t n,
+                                                               uint64_t s0, double mu, double sigma,
+                                                               int64_t offset) {
+#pragma clang fp contract(off)
+    const uint64_t gamma = 0x9E3779B97F4A7C15ull;
+    const double two_pi = 6.283185307179586476925286766559;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t first_pair = offset >> 1;
+    const int64_t last_pair = (offset + n - 1) >> 1;
+    for (int64_t j = first_pair + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j <= last_pair;
+         j += stride) {
+        const uint64_t a = sm64_mix(s0 + (uint64_t)(2 * j + 1) * gamma);
+        const uint64_t b = sm64_mix(s0 + (uint64_t)(2 * j + 2) * gamma);
+        const double u1 = (double)((a >> 11) + 1) * (1.0 / 9007199254740992.0);
+        const double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
+        const double r = sqrt(-2.0 * log(u1));
+        const double t = two_pi * u2;
+        const int64_t e0 = 2 * j - offset;
+        if (e0 >= 0 && e0 < n) out[e0] = (uint16_t)f64_to_bf16(mu + sigma * (r * cos(t)));
+        if (e0 + 1 >= 0 && e0 + 1 < n) out[e0 + 1] = (uint16_t)f64_to_bf16(mu + sigma * (r * sin(t)));
+    }
+}
+
+static int grid_for(int64_t work_items, int block, int max_blocks) {
+    int64_t g = (work_items + block - 1) / block;
+    if (g > max_blocks) g = max_blocks;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+}  // namespace mq4
+
+using namespace mq4;
+
+extern "C" int mq4_quantize(const uint16_t* w, int64_t N, int64_t K, int group_size, int bits,
+                            uint32_t* wq, uint16_t* scales, uint16_t* biases, void* stream) {
+    const char* what = "mq4_quantize";
+    if (int rc = check_format(what, group_size, bits)) return rc;
+    if (int rc = check_k(what, K)) return rc;
+    if (N <= 0) return fail(MQ4_ERR_INVALID_ARG, "%s: N=%lld must be positive", what, (long long)N);
+    if (!w || !wq || !scales || !biases) return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
+    if (!aligned(w, 16) || !aligned(wq, 4) || !aligned(scales, 2) || !aligned(biases, 2))
+        return fail(MQ4_ERR_ALIGNMENT, "%s: w must be 16-byte aligned, wq 4-byte, scales/biases 2-byte",
+                    what);
+    const int64_t n_words = N * (K / 8);
+    const int block = 256;
+    const int grid = grid_for(n_words, block, 256 * 32);
+    hipLaunchKernelGGL(quantize_g64_kernel, dim3(grid), dim3(block), 0, as_stream(stream),
+                       reinterpret_cast<const uint4*>(w), n_words, wq, scales, biases);
+    return launch_status(what);
+}
+
+extern "C" int mq4_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                              int64_t N, int64_t K, int group_size, int bits, void* out, int out_f32,
+                              void* stream) {
+    const char* what = "mq4_dequantize";
+    if (int rc = check_format(what, group_size, bits)) return rc;
+    if (int rc = check_k(what, K)) return rc;
+    if (N <= 0) return fail(MQ4_ERR_INVALID_ARG, "%s: N=%lld must be positive", what, (long long)N);
+    if (!wq || !scales || !biases || !out) return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
+    if (!aligned(wq, 4) || !aligned(scales, 2) || !aligned(biases, 2) || !aligned(out, 16))
+        return fail(MQ4_ERR_ALIGNMENT, "%s: out must be 16-byte aligned, wq 4-byte", what);
+    const int64_t n_words = N * (K / 8);
+    const int block = 256;
+    const int grid = grid_for(n_words, block, 256 * 32);
+    if (out_f32)
+        hipLaunchKernelGGL(dequantize_g64_kernel<true>, dim3(grid), dim3(block), 0, as_stream(stream),
+                           wq, scales, biases, n_words, out);
+    else
+        hipLaunchKernelGGL(dequantize_g64_kernel<false>, dim3(grid), dim3(block), 0, as_stream(stream),
+                           wq, scales, biases, n_words, out);
+    return launch_status(what);
+}
+
+extern "C" int mq4_fill_normal_bf16(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream_id,
+                                    double mu, double sigma, int64_t offset, void* stream) {
+    const char* what = "mq4_fill_normal_bf16";
+    if (!out) return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
+    if (n < 0 || offset < 0) return fail(MQ4_ERR_INVALID_ARG, "%s: negative n or offset", what);
+    if (n == 0) return ok();
+    const int64_t pairs = ((offset + n - 1) >> 1) - (offset >> 1) + 1;
+    const int block = 256;
+    const int grid = grid_for(pairs, block, 256 * 64);
+    hipLaunchKernelGGL(fill_normal_bf16_kernel, dim3(grid), dim3(block), 0, as_stream(stream), out, n,
+                       seed ^ stream_id, mu, sigma, offset);
+    return launch_status(what);
+}

@@ -1,0 +1,211 @@
+"""ctypes + numpy front end of the CPU oracle (libmq4_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker (or the timed CPU
+baseline), never as the product.  The product path (libmq4.so) does not load
+anything from this directory.
+
+Every function mirrors one in mq4_oracle.c; that file's header names the
+reference file:line each follows.  Arrays of bf16 values are numpy uint16
+holding the raw bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libmq4_oracle.so")
+_lib = None
+
+GROUP = 64
+BITS = 4
+SEED = 0x4D41524C  # "MARL"
+
+
+def build() -> None:
+    """Compile libmq4_oracle.so with the Makefile beside this file."""
+    subprocess.check_call(["make", "-s", "-C", _HERE])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        L.mq4o_gen_normal_bf16.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double,
+                                           ctypes.c_double, I64, I64, P]
+        L.mq4o_quantize.argtypes = [P, I64, I64, P, P, P]
+        L.mq4o_quantize.restype = ctypes.c_int
+        L.mq4o_dequantize_f64.argtypes = [P, P, P, I64, I64, P]
+        L.mq4o_qmm_f64.argtypes = [P, I64, I64, P, P, P, I64, P, P]
+        L.mq4o_qmm_f32.argtypes = [P, I64, I64, P, P, P, I64, P]
+        L.mq4o_qmm_mlx_bf16.argtypes = [P, I64, I64, P, P, P, I64, P]
+        L.mq4o_swiglu_bf16.argtypes = [P, P, I64, P]
+        L.mq4o_argmax_bf16.argtypes = [P, I64, I64, P]
+        L.mq4o_rmsnorm_1pw.argtypes = [P, P, I64, I64, ctypes.c_float, P]
+        L.mq4o_add_bf16.argtypes = [P, P, I64, P]
+        L.mq4o_f32_to_bf16_array.argtypes = [P, P, I64]
+        L.mq4o_f64_to_bf16_array.argtypes = [P, P, I64]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ------------------------------------------------------------------ bf16 ---
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().mq4o_f32_to_bf16_array(_p(f), _p(out), f.size)
+    return out
+
+
+def f64_to_bf16(d: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(d, dtype=np.float64)
+    out = np.empty(d.shape, np.uint16)
+    lib().mq4o_f64_to_bf16_array(_p(d), _p(out), d.size)
+    return out
+
+
+# ------------------------------------------------------------- generator ---
+def gen_normal_bf16(stream_id: int, n: int, mu: float = 0.0, sigma: float = 1.0,
+                    seed: int = SEED, offset: int = 0) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    lib().mq4o_gen_normal_bf16(seed, stream_id, mu, sigma, offset, n, _p(out))
+    return out
+
+
+# -------------------------------------------------------------- quantize ---
+def quantize(w: np.ndarray):
+    """w: uint16 bf16 bits [N, K] -> (wq uint32 [N, K/8], scales, biases uint16 [N, K/64])."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    N, K = w.shape
+    wq = np.empty((N, K // 8), np.uint32)
+    s = np.empty((N, K // GROUP), np.uint16)
+    b = np.empty((N, K // GROUP), np.uint16)
+    rc = lib().mq4o_quantize(_p(w), N, K, _p(wq), _p(s), _p(b))
+    if rc != 0:
+        raise ValueError(f"oracle quantize: K={K} must be a positive multiple of {GROUP}")
+    return wq, s, b
+
+
+def dequantize_f64(wq, s, b) -> np.ndarray:
+    N = wq.shape[0]
+    K = wq.shape[1] * 8
+    out = np.empty((N, K), np.float64)
+    lib().mq4o_dequantize_f64(_p(np.ascontiguousarray(wq)), _p(np.ascontiguousarray(s)),
+                              _p(np.ascontiguousarray(b)), N, K, _p(out))
+    return out
+
+
+# ------------------------------------------------------------------- qmm ---
+def _qmm_args(x, wq, s, b):
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    if x.ndim == 1:
+        x = x[None, :]
+    M, K = x.shape
+    N = wq.shape[0]
+    assert wq.shape == (N, K // 8) and s.shape == (N, K // GROUP) and b.shape == s.shape
+    return x, M, K, N, np.ascontiguousarray(wq), np.ascontiguousarray(s), np.ascontiguousarray(b)
+
+
+def qmm_f64(x, wq, s, b):
+    """fp64 oracle: returns (y_f64 [M, N], y_bf16 [M, N] = RNE(y_f64))."""
+    x, M, K, N, wq, s, b = _qmm_args(x, wq, s, b)
+    y = np.empty((M, N), np.float64)
+    yb = np.empty((M, N), np.uint16)
+    lib().mq4o_qmm_f64(_p(x), M, K, _p(wq), _p(s), _p(b), N, _p(y), _p(yb))
+    return y, yb
+
+
+def qmm_f32(x, wq, s, b):
+    x, M, K, N, wq, s, b = _qmm_args(x, wq, s, b)
+    yb = np.empty((M, N), np.uint16)
+    lib().mq4o_qmm_f32(_p(x), M, K, _p(wq), _p(s), _p(b), N, _p(yb))
+    return yb
+
+
+def qmm_mlx_bf16(x, wq, s, b):
+    x, M, K, N, wq, s, b = _qmm_args(x, wq, s, b)
+    yb = np.empty((M, N), np.uint16)
+    lib().mq4o_qmm_mlx_bf16(_p(x), M, K, _p(wq), _p(s), _p(b), N, _p(yb))
+    return yb
+
+
+# ---------------------------------------------------- swiglu/argmax/norm ---
+def swiglu_bf16(g, u):
+    g = np.ascontiguousarray(g, dtype=np.uint16)
+    u = np.ascontiguousarray(u, dtype=np.uint16)
+    out = np.empty(g.shape, np.uint16)
+    lib().mq4o_swiglu_bf16(_p(g), _p(u), g.size, _p(out))
+    return out
+
+
+def argmax_bf16(logits):
+    logits = np.ascontiguousarray(logits, dtype=np.uint16)
+    if logits.ndim == 1:
+        logits = logits[None, :]
+    M, N = logits.shape
+    idx = np.empty(M, np.uint32)
+    lib().mq4o_argmax_bf16(_p(logits), M, N, _p(idx))
+    return idx
+
+
+def rmsnorm_1pw(x, w, eps: float = 1e-6):
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    if x.ndim == 1:
+        x = x[None, :]
+    M, K = x.shape
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    out = np.empty((M, K), np.uint16)
+    lib().mq4o_rmsnorm_1pw(_p(x), _p(w), M, K, eps, _p(out))
+    return out
+
+
+def add_bf16(a, b):
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    out = np.empty(a.shape, np.uint16)
+    lib().mq4o_add_bf16(_p(a), _p(b), a.size, _p(out))
+    return out
+
+
+def mlp_forward(x, gate, up, down):
+    """down(swiglu(gate x, up x)) with each qmm rounded once from fp64 to bf16
+    (src/model/marlin.cpp:31-35); gate/up/down are (wq, s, b) triples."""
+    _, g = qmm_f64(x, *gate)
+    _, u = qmm_f64(x, *up)
+    h = swiglu_bf16(g, u)
+    _, y = qmm_f64(h, *down)
+    return g, u, h, y
+
+
+# ---------------------------------------------------- tolerance helpers ---
+def rel_rms_err(got_bf16, ref_f64) -> float:
+    """max |got - ref| / rms(ref) with got as bf16 bits, ref as fp64 values."""
+    g = bf16_to_f32(np.asarray(got_bf16)).astype(np.float64)
+    r = np.asarray(ref_f64, dtype=np.float64)
+    rms = float(np.sqrt(np.mean(r * r)))
+    return float(np.max(np.abs(g - r)) / rms) if rms > 0 else float(np.max(np.abs(g - r)))
+
+
+def bf16_ulp_diff(a_bf16, b_bf16) -> np.ndarray:
+    """Distance in bf16 ulps between two bf16 bit arrays (monotone integer map)."""
+    def key(h):
+        h = np.asarray(h, dtype=np.uint16).astype(np.int32)
+        return np.where(h & 0x8000, 0x8000 - (h & 0x7FFF), 0x8000 + h)
+    return np.abs(key(a_bf16) - key(b_bf16))

@@ -1,0 +1,109 @@
+"""C-ABI surface of libmq4.so, checked without a GPU: the library loads, it
+exports every function include/mq4.h declares, and argument validation
+rejects bad calls with the documented status codes before any HIP call."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mq4.h")
+
+OK, INVALID, UNSUPPORTED, ALIGN, HIPERR, WORKSPACE = 0, -1, -2, -3, -4, -5
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mq4_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for must in ("mq4_quantize", "mq4_qmm", "mq4_mlp_gate_up_silu", "mq4_lm_head_argmax",
+                 "mq4_argmax_bf16", "mq4_qmm_residual", "mq4_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(mq4):
+    L = mq4.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), f"libmq4.so does not export {name}"
+    assert L.mq4_version() >= 100
+
+
+def fake(addr):
+    """A non-null 'device pointer' with the given alignment; never dereferenced
+    because every call below fails validation first."""
+    return ctypes.c_void_p(addr)
+
+
+A16 = 0x100000
+S = ctypes.c_void_p(0)
+
+
+def last_error(mq4):
+    return mq4.lib().mq4_last_error().decode()
+
+
+def test_quantize_validation(mq4):
+    L = mq4.lib()
+    assert L.mq4_quantize(fake(A16), 4, 128, 32, 4, fake(A16), fake(A16), fake(A16), S) == UNSUPPORTED
+    assert "group_size" in last_error(mq4)
+    assert L.mq4_quantize(fake(A16), 4, 128, 64, 8, fake(A16), fake(A16), fake(A16), S) == UNSUPPORTED
+    assert L.mq4_quantize(fake(A16), 4, 96, 64, 4, fake(A16), fake(A16), fake(A16), S) == INVALID
+    assert L.mq4_quantize(fake(A16), 0, 128, 64, 4, fake(A16), fake(A16), fake(A16), S) == INVALID
+    assert L.mq4_quantize(None, 4, 128, 64, 4, fake(A16), fake(A16), fake(A16), S) == INVALID
+    assert L.mq4_quantize(fake(A16 + 8), 4, 128, 64, 4, fake(A16), fake(A16), fake(A16), S) == ALIGN
+    assert L.mq4_quantize(fake(A16), 4, 128, 64, 4, fake(A16 + 2), fake(A16), fake(A16), S) == ALIGN
+
+
+def test_qmm_validation(mq4):
+    L = mq4.lib()
+    args = lambda **kw: [kw.get("x", fake(A16)), kw.get("M", 1), kw.get("K", 2048), kw.get("wq", fake(A16)),
+                         fake(A16), fake(A16), kw.get("N", 64), kw.get("tr", 1), kw.get("g", 64),
+                         kw.get("bits", 4), kw.get("y", fake(A16)), S]
+    assert L.mq4_qmm(*args(tr=0)) == UNSUPPORTED
+    assert "transpose" in last_error(mq4)
+    assert L.mq4_qmm(*args(g=128)) == UNSUPPORTED
+    assert L.mq4_qmm(*args(K=100)) == INVALID
+    assert L.mq4_qmm(*args(K=65536 + 64)) == UNSUPPORTED
+    assert L.mq4_qmm(*args(M=0)) == INVALID
+    assert L.mq4_qmm(*args(N=0)) == INVALID
+    assert L.mq4_qmm(*args(x=fake(A16 + 2))) == ALIGN
+    assert L.mq4_qmm(*args(wq=fake(A16 + 4))) == ALIGN
+    assert L.mq4_qmm(*args(y=None)) == INVALID
+
+
+def test_lm_head_workspace_validation(mq4):
+    L = mq4.lib()
+    need = L.mq4_lm_head_argmax_workspace_size(1, 248320)
+    assert need > 0 and L.mq4_lm_head_argmax_workspace_size(4, 248320) == 4 * need
+    rc = L.mq4_lm_head_argmax(fake(A16), 1, 2048, fake(A16), fake(A16), fake(A16), 248320,
+                              fake(A16), None, fake(A16), need - 8, S)
+    assert rc == WORKSPACE
+    rc = L.mq4_lm_head_argmax(fake(A16), 1, 2048, fake(A16), fake(A16), fake(A16), 248320,
+                              fake(A16), None, None, need, S)
+    assert rc == WORKSPACE
+    rc = L.mq4_argmax_bf16(fake(A16), 1, 10, fake(A16), fake(A16), 0, S)
+    assert rc == WORKSPACE
+
+
+def test_error_message_is_per_call(mq4):
+    L = mq4.lib()
+    L.mq4_quantize(fake(A16), 4, 128, 32, 4, fake(A16), fake(A16), fake(A16), S)
+    assert last_error(mq4) != ""
+    # a successful zero-length call clears it
+    assert L.mq4_swiglu_bf16(fake(A16), fake(A16), 0, fake(A16), S) == OK
+    assert last_error(mq4) == ""
+
+
+def test_python_api_rejects_host_tensors(mq4):
+    import torch
+    with pytest.raises(ValueError):
+        mq4.quantize(torch.zeros(4, 64, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        mq4.quantize(torch.zeros(4, 64, dtype=torch.float32))
+    with pytest.raises(NotImplementedError):
+        mq4.sample_token(torch.zeros(1, 1, 8, dtype=torch.bfloat16), temperature=0.7)

@@ -1,0 +1,299 @@
+"""GPU parity of libmq4 (called through its C ABI via the package's ctypes
+bindings) against the CPU oracle on identical seeded inputs.
+
+Bars (stated per test):
+* quantize / pack, scales, biases, argmax indices: bit-exact.
+* GEMV / fused outputs (bf16): max |got - ref| <= 1e-2 * rms(ref) with ref the
+  fp64 oracle, and at most 1 bf16 ulp from bf16(fp64) element-wise.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev_bf16, to_host_u16
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2   # max |err| relative to the reference output's RMS
+
+
+def words(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def gen_weight(mq4, O, stream_id, N, K, sigma=0.02, dev="cuda:0"):
+    """Generate on the GPU (fast) and return (device tensor, host bits)."""
+    w = mq4.fill_normal_bf16((N, K), stream_id, 0.0, sigma, device=dev)
+    return w, to_host_u16(w)
+
+
+def check_close(O, got_bits, ref64, what):
+    ref_b = O.f64_to_bf16(ref64)
+    err = O.rel_rms_err(got_bits, ref64)
+    ulp = int(O.bf16_ulp_diff(got_bits, ref_b).max())
+    assert err <= TOL, f"{what}: max|err|/rms = {err:.3e}"
+    assert ulp <= 1, f"{what}: {ulp} bf16 ulps from bf16(fp64)"
+    return err
+
+
+# ---------------------------------------------------------- generator ---
+
+@pytest.mark.parametrize("sid,n,mu,sigma,off", [(1000, 65536, 0.0, 0.02, 0), (2000, 4097, 0.0, 0.02, 12345),
+                                               (2001, 2048, 0.1, 0.02, 0), (3000, 2048, 0.0, 1.0, 0)])
+def test_generator_gpu_matches_cpu(mq4, O, dev, sid, n, mu, sigma, off):
+    g = to_host_u16(mq4.fill_normal_bf16((n,), sid, mu, sigma, device=dev, offset=off))
+    assert np.array_equal(g, O.gen_normal_bf16(sid, n, mu, sigma, offset=off))
+
+
+# ----------------------------------------------------------- quantize ---
+
+def test_quantize_known_answers(mq4, O, dev):
+    import json, os
+    cases = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "quantize_kat.json")))["cases"]
+    groups = []
+    for c in cases:
+        v = np.full(64, c["fill"], np.float32)
+        for k, val in c["set"].items():
+            v[int(k)] = val
+        groups.append(O.f32_to_bf16(v))
+    w = np.stack(groups)                 # one KAT group per row
+    wq, s, b = mq4.quantize(to_dev_bf16(w, dev))
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        assert [f"0x{x:08x}" for x in words(wq)[i]] == c["words"], c["name"]
+        assert f"0x{to_host_u16(s)[i, 0]:04x}" == c["scale"], c["name"]
+        assert f"0x{to_host_u16(b)[i, 0]:04x}" == c["bias"], c["name"]
+
+
+@pytest.mark.parametrize("N,K,sid", [(6144, 2048, 1000), (2048, 6144, 1002), (248320, 2048, 2000),
+                                     (1, 64, 5), (3, 192, 6), (7, 4160, 7)])
+def test_quantize_bit_exact(mq4, O, dev, N, K, sid):
+    print(f"quantize N={N} K={K}", flush=True)
+    w, wh = gen_weight(mq4, O, sid, N, K)
+    wq, s, b = mq4.quantize(w)
+    torch.cuda.synchronize()
+    rq, rs, rb = O.quantize(wh)
+    assert np.array_equal(words(wq), rq)
+    assert np.array_equal(to_host_u16(s), rs)
+    assert np.array_equal(to_host_u16(b), rb)
+
+
+def test_quantize_planted_ties_and_special_groups(mq4, O, dev):
+    """Random rows with exact-.5 tie groups, constant groups, all-zero groups and
+    wide-range (clipping) groups planted at random positions."""
+    N, K = 512, 2048
+    wh = O.gen_normal_bf16(77, N * K, 0.0, 0.02).reshape(N, K).copy()
+    ties = O.f32_to_bf16(np.array([-1.875, 0.0, -1.8125, -1.6875, -1.5625, -1.4375, -0.0625] + [-1.0] * 57,
+                                  np.float32))
+    rng = np.random.default_rng(5)
+    for n, g in zip(rng.integers(0, N, 200), rng.integers(0, K // 64, 200)):
+        kind = rng.integers(0, 4)
+        blk = wh[n, 64 * g:64 * g + 64]
+        if kind == 0:
+            blk[:] = rng.permutation(ties)
+        elif kind == 1:
+            blk[:] = O.f32_to_bf16(np.full(64, rng.standard_normal() * 0.02, np.float32))
+        elif kind == 2:
+            blk[:] = 0
+        else:
+            blk[rng.integers(0, 64)] = O.f32_to_bf16(np.array([rng.standard_normal() * 2.0], np.float32))[0]
+    wq, s, b = mq4.quantize(to_dev_bf16(wh, dev))
+    torch.cuda.synchronize()
+    rq, rs, rb = O.quantize(wh)
+    assert np.array_equal(words(wq), rq)
+    assert np.array_equal(to_host_u16(s), rs)
+    assert np.array_equal(to_host_u16(b), rb)
+
+
+def test_dequantize_matches_affine_formula(mq4, O, dev):
+    N, K = 96, 2048
+    w, wh = gen_weight(mq4, O, 9, N, K)
+    wq, s, b = mq4.quantize(w)
+    d32 = mq4.dequantize(wq, s, b, dtype=torch.float32).cpu().numpy().astype(np.float64)
+    d16 = to_host_u16(mq4.dequantize(wq, s, b))
+    ref = O.dequantize_f64(*O.quantize(wh))
+    assert np.array_equal(d32, ref)              # s*q + b is exact in float for these data
+    assert np.array_equal(d16, O.f64_to_bf16(ref))
+
+
+# --------------------------------------------------------------- GEMV ---
+
+QMM_SHAPES = [
+    (1, 6144, 2048), (1, 2048, 6144), (2, 6144, 2048), (3, 100, 2048), (4, 2048, 6144),
+    (5, 64, 1024), (8, 33, 4096), (16, 512, 2048), (32, 256, 2048), (1, 7, 64), (1, 1, 64),
+    (2, 130, 128), (1, 64, 16384), (1, 32, 20480), (2, 8, 20480), (3, 50, 8256),
+]
+
+
+@pytest.mark.parametrize("M,N,K", QMM_SHAPES)
+def test_qmm_matches_fp64_oracle(mq4, O, dev, M, N, K):
+    print(f"qmm M={M} N={N} K={K}", flush=True)
+    w, wh = gen_weight(mq4, O, 1000 + N % 97, N, K)
+    xh = O.gen_normal_bf16(3000 + M, M * K).reshape(M, K)
+    qt = mq4.quantize_weight(w)
+    y = mq4.qmatmul(to_dev_bf16(xh, dev), qt)
+    torch.cuda.synchronize()
+    ref, _ = O.qmm_f64(xh, *O.quantize(wh))
+    check_close(O, to_host_u16(y), ref, f"qmm {M}x{N}x{K}")
+
+
+def test_qmm_batched_leading_dims(mq4, O, dev):
+    """x of shape [1, S, K] like the reference's [1, M, K] activations."""
+    S, N, K = 6, 300, 2048
+    w, wh = gen_weight(mq4, O, 1234, N, K)
+    xh = O.gen_normal_bf16(4000, S * K).reshape(S, K)
+    qt = mq4.quantize_weight(w)
+    y = mq4.qmatmul(to_dev_bf16(xh, dev).view(1, S, K), qt)
+    assert y.shape == (1, S, N)
+    ref, _ = O.qmm_f64(xh, *O.quantize(wh))
+    check_close(O, to_host_u16(y).reshape(S, N), ref, "qmm [1,S,K]")
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 5])
+def test_mlp_gate_up_silu(mq4, O, dev, M):
+    N, K = 6144, 2048
+    wg, wgh = gen_weight(mq4, O, 1000, N, K)
+    wu, wuh = gen_weight(mq4, O, 1001, N, K)
+    xh = O.gen_normal_bf16(3000, M * K).reshape(M, K)
+    qg, qu = mq4.quantize_weight(wg), mq4.quantize_weight(wu)
+    h = mq4.mlp_gate_up_silu(to_dev_bf16(xh, dev), qg, qu)
+    torch.cuda.synchronize()
+    g64, gb = O.qmm_f64(xh, *O.quantize(wgh))
+    u64, ub = O.qmm_f64(xh, *O.quantize(wuh))
+    href = O.swiglu_bf16(gb, ub)
+    # reference h from bf16(fp64) g and u; compare within the tolerance
+    err = O.rel_rms_err(to_host_u16(h), O.bf16_to_f32(href).astype(np.float64))
+    assert err <= TOL
+    # the fused kernel equals the unfused ops on its own g and u up to the
+    # rounding of g/u: check against qmm + swiglu from this library
+    g = mq4.qmatmul(to_dev_bf16(xh, dev), qg)
+    u = mq4.qmatmul(to_dev_bf16(xh, dev), qu)
+    h2 = mq4.swiglu(g, u)
+    d = O.bf16_ulp_diff(to_host_u16(h), to_host_u16(h2))
+    assert d.max() <= 4 and np.mean(d > 0) < 0.01
+    # the device expf and libm's may differ in the last float ulp, which can
+    # flip a bf16 rounding of sigmoid for a few elements
+    d2 = O.bf16_ulp_diff(to_host_u16(h2), O.swiglu_bf16(to_host_u16(g), to_host_u16(u)))
+    assert d2.max() <= 2 and np.mean(d2 > 0) < 1e-3
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_qmm_residual_in_place(mq4, O, dev, M):
+    N, K = 2048, 6144
+    w, wh = gen_weight(mq4, O, 1002, N, K)
+    hh = O.gen_normal_bf16(3100, M * K, 0.0, 0.3).reshape(M, K)
+    rh = O.gen_normal_bf16(3200, M * N).reshape(M, N)
+    qt = mq4.quantize_weight(w)
+    r = to_dev_bf16(rh, dev)
+    out = mq4.qmatmul_residual(to_dev_bf16(hh, dev), qt, r, out=r)   # in place
+    torch.cuda.synchronize()
+    assert out.data_ptr() == r.data_ptr()
+    y64, yb = O.qmm_f64(hh, *O.quantize(wh))
+    ref = O.add_bf16(rh, yb)
+    got = to_host_u16(r)
+    assert O.bf16_ulp_diff(got, ref).max() <= 1
+    assert O.rel_rms_err(got, O.bf16_to_f32(ref).astype(np.float64)) <= TOL
+
+
+def test_mlp_chain_two_layers(mq4, O, dev):
+    """hidden = hidden + mlp(hidden) twice (src/model/marlin.cpp:142), M=1."""
+    N, K = 6144, 2048
+    layers_d, layers_h = [], []
+    for l in range(2):
+        ws = [gen_weight(mq4, O, mq4.stream_id_layer(l, p), *((N, K) if p < 2 else (K, N))) for p in range(3)]
+        layers_d.append(mq4.MLPWeights(*[mq4.quantize_weight(w) for w, _ in ws]))
+        layers_h.append([O.quantize(h) for _, h in ws])
+    xh = O.gen_normal_bf16(3000, K).reshape(1, K)
+    x = to_dev_bf16(xh, dev)
+    for lw in layers_d:
+        x = mq4.mlp_forward(x, lw, residual=x)
+    torch.cuda.synchronize()
+    ref = xh
+    for g, u, d in layers_h:
+        _, _, _, y = O.mlp_forward(ref, g, u, d)
+        ref = O.add_bf16(ref, y)
+    err = O.rel_rms_err(to_host_u16(x), O.bf16_to_f32(ref).astype(np.float64))
+    assert err <= TOL
+
+
+# ------------------------------------------------------ lm_head/argmax ---
+
+@pytest.fixture(scope="module")
+def lm_head(mq4, O, dev):
+    V, K = 248320, 2048
+    w, wh = gen_weight(mq4, O, mq4.STREAM_LM_HEAD, V, K)
+    qt = mq4.quantize_weight(w)
+    torch.cuda.synchronize()
+    return qt, O.quantize(wh)
+
+
+def normed_hidden(O, M, K=2048):
+    x = O.gen_normal_bf16(3000, M * K).reshape(M, K)
+    nw = O.gen_normal_bf16(2001, K, 0.1, 0.02)
+    return O.rmsnorm_1pw(x, nw)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_lm_head_argmax_full_vocab(mq4, O, dev, lm_head, M):
+    qt, (rq, rs, rb) = lm_head
+    hh = normed_hidden(O, M)
+    idx, logits = mq4.lm_head_argmax(to_dev_bf16(hh, dev), qt, return_logits=True)
+    torch.cuda.synchronize()
+    lg = to_host_u16(logits)
+    ref64, refb = O.qmm_f64(hh, rq, rs, rb)
+    check_close(O, lg, ref64, "lm_head logits")
+    got = idx.cpu().numpy().astype(np.uint32)
+    # argmax semantics are bit-exact on the kernel's own logits
+    assert np.array_equal(got, O.argmax_bf16(lg))
+    # and equal to the argmax of bf16(fp64) logits unless that row's top two
+    # bf16 values are within one ulp (a near-tie the rounding may flip)
+    ref_idx = O.argmax_bf16(refb)
+    for m in range(M):
+        if got[m] != ref_idx[m]:
+            top = np.sort(O.bf16_to_f32(refb[m]))[-2:]
+            assert O.bf16_ulp_diff(O.f32_to_bf16(top[:1]), O.f32_to_bf16(top[1:]))[0] <= 1
+    # the fused path equals the unfused lm_head + argmax
+    idx2 = mq4.argmax(logits)
+    assert np.array_equal(idx2.cpu().numpy(), idx.cpu().numpy())
+
+
+def test_lm_head_argmax_planted_tie(mq4, O, dev):
+    """Duplicate the winning row at an earlier and at a later index: the
+    lowest index must win (mx::argmax first-occurrence rule)."""
+    V, K = 40000, 2048
+    w, wh = gen_weight(mq4, O, 2000, V, K)
+    hh = normed_hidden(O, 1)
+    qt = mq4.quantize_weight(w)
+    i0 = int(mq4.lm_head_argmax(to_dev_bf16(hh, dev), qt).cpu()[0])
+    for dst in (17, V - 3):
+        if dst == i0:
+            continue
+        wh2 = wh.copy()
+        wh2[dst] = wh[i0]        # identical rows give bit-identical logits
+        idx = mq4.lm_head_argmax(to_dev_bf16(hh, dev), mq4.quantize_weight(to_dev_bf16(wh2, dev)))
+        assert int(idx.cpu()[0]) == min(dst, i0)
+
+
+def test_argmax_special_values(mq4, O, dev):
+    rng = np.random.default_rng(9)
+    M, N = 5, 300000
+    v = rng.standard_normal((M, N)).astype(np.float32)
+    v[0, [5, 200000]] = 40.0
+    v[1, :] = -3.0
+    v[2, 123456] = 1e30
+    bits = O.f32_to_bf16(v)
+    bits[3, :] = 0x8000
+    bits[3, 77] = 0x0000          # +0 vs -0: equal, so index 0 wins
+    bits[4, 10] = 0x7fc0          # NaN never wins
+    bits[4, 11] = O.f32_to_bf16(np.array([100.0], np.float32))[0]
+    idx = mq4.argmax(to_dev_bf16(bits, dev))
+    got = idx.cpu().numpy().astype(np.uint32)
+    assert np.array_equal(got, O.argmax_bf16(bits))
+    assert list(got) == [5, 0, 123456, 0, 11]
+
+
+def test_sample_token_greedy_last_row(mq4, O, dev):
+    S, V = 3, 1000
+    bits = O.gen_normal_bf16(42, S * V).reshape(1, S, V)
+    tok = mq4.sample_token(to_dev_bf16(bits, dev), temperature=0.0)
+    assert int(tok.cpu().reshape(-1)[0]) == int(O.argmax_bf16(bits[0, -1])[0])
