@@ -90,6 +90,13 @@ int mq4_qmm(const uint16_t* x, int64_t M, int64_t K,
             const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int64_t N,
             int transpose, int group_size, int bits, uint16_t* y, void* stream);
 
+/* Same product as mq4_qmm with the fp32 accumulator stored unrounded in
+ * y (float [M, N]): for accuracy checks against an fp64 reference and for
+ * callers that keep fp32 outputs.  y must be 4-byte aligned. */
+int mq4_qmm_f32(const uint16_t* x, int64_t M, int64_t K,
+                const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int64_t N,
+                float* y, void* stream);
+
 /* y = bf16(residual + bf16(x @ W^T)): the down projection with the residual
  * add that follows it (src/model/marlin.cpp:34 and :142).  residual [M, N]
  * may alias y (in-place update of the hidden state). */

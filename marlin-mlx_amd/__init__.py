@@ -28,7 +28,7 @@ import torch
 
 __all__ = [
     "MQ4Error", "library_path", "lib", "QuantizedTensor", "MLPWeights",
-    "quantize", "dequantize", "quantized_matmul", "argmax", "swiglu",
+    "quantize", "dequantize", "quantized_matmul", "quantized_matmul_f32", "argmax", "swiglu",
     "quantize_weight", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
     "lm_head", "lm_head_argmax", "sample_token", "fill_normal_bf16",
 ]
@@ -89,6 +89,7 @@ def lib():
         "mq4_dequantize": ([P, P, P, I64, I64, I, I, P, I, P], I),
         "mq4_qmm": ([P, I64, I64, P, P, P, I64, I, I, I, P, P], I),
         "mq4_qmm_residual": ([P, I64, I64, P, P, P, I64, P, P, P], I),
+        "mq4_qmm_f32": ([P, I64, I64, P, P, P, I64, P, P], I),
         "mq4_mlp_gate_up_silu": ([P, I64, I64, P, P, P, P, P, P, I64, P, P], I),
         "mq4_swiglu_bf16": ([P, P, I64, P, P], I),
         "mq4_lm_head_argmax_workspace_size": ([I64, I64], SZ),
@@ -179,6 +180,22 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     M, K, y = _mk(x, N)
     _check(lib().mq4_qmm(_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N, int(transpose),
                          group_size, bits, _ptr(y), _stream(x.device)))
+    return y
+
+
+def quantized_matmul_f32(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                         biases: torch.Tensor) -> torch.Tensor:
+    """quantized_matmul with the fp32 accumulator returned unrounded (float32)."""
+    x = _need(x, torch.bfloat16, "x")
+    w = _need(w, torch.int32, "w")
+    scales = _need(scales, torch.bfloat16, "scales")
+    biases = _need(biases, torch.bfloat16, "biases")
+    N = w.shape[0]
+    K = x.shape[-1]
+    M = x.numel() // K
+    y = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=x.device)
+    _check(lib().mq4_qmm_f32(_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N, _ptr(y),
+                             _stream(x.device)))
     return y
 
 

@@ -28,7 +28,7 @@
 
 namespace mq4 {
 
-enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3, EPI_STORE_F32 = 4 };
 
 struct QMat {
     const uint32_t* wq;
@@ -201,6 +201,8 @@ __global__ __launch_bounds__(64 * KS) void q4_gemv_kernel(
         const bool live = holder && row < N && m < m_valid && (EPI != EPI_SWIGLU || t_mat == 0);
         if (EPI == EPI_STORE) {
             if (live) y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16(val);
+        } else if (EPI == EPI_STORE_F32) {
+            if (live) reinterpret_cast<float*>(y)[(int64_t)m * N + row] = val;
         } else if (EPI == EPI_RESIDUAL) {
             if (live) {
                 const float rsd = bf16_to_f32(res[(int64_t)m * N + row]);
@@ -346,7 +348,7 @@ static int run_gemv(const GemvArgs& base, int M, hipStream_t st) {
         const int mc = (M - m0) < chunk ? (M - m0) : chunk;
         a.x = base.x + (int64_t)m0 * base.K;
         a.m_valid = mc;
-        if (base.y) a.y = base.y + (int64_t)m0 * base.N;
+        if (base.y) a.y = base.y + (int64_t)m0 * base.N * (EPI == EPI_STORE_F32 ? 2 : 1);
         if (base.res) a.res = base.res + (int64_t)m0 * base.N;
         if (base.partial) a.partial = base.partial + (int64_t)m0 * kMaxGemvBlocks;
         int rc;
@@ -391,6 +393,19 @@ extern "C" int mq4_qmm(const uint16_t* x, int64_t M, int64_t K, const uint32_t* 
     GemvArgs a{x, (int)M, {wq, scales, biases}, {nullptr, nullptr, nullptr}, (int)N, (int)K, y, nullptr,
                nullptr};
     if (run_gemv<EPI_STORE>(a, (int)M, as_stream(stream)))
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
+    return launch_status(what);
+}
+
+extern "C" int mq4_qmm_f32(const uint16_t* x, int64_t M, int64_t K, const uint32_t* wq,
+                           const uint16_t* scales, const uint16_t* biases, int64_t N, float* y,
+                           void* stream) {
+    const char* what = "mq4_qmm_f32";
+    if (int rc = check_qmm_args(what, x, M, K, wq, scales, biases, N)) return rc;
+    if (!y || !aligned(y, 4)) return fail(MQ4_ERR_INVALID_ARG, "%s: y must be a 4-byte aligned pointer", what);
+    GemvArgs a{x, (int)M, {wq, scales, biases}, {nullptr, nullptr, nullptr}, (int)N, (int)K,
+               reinterpret_cast<uint16_t*>(y), nullptr, nullptr};
+    if (run_gemv<EPI_STORE_F32>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }

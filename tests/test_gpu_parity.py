@@ -3,8 +3,14 @@ bindings) against the CPU oracle on identical seeded inputs.
 
 Bars (stated per test):
 * quantize / pack, scales, biases, argmax indices: bit-exact.
-* GEMV / fused outputs (bf16): max |got - ref| <= 1e-2 * rms(ref) with ref the
-  fp64 oracle, and at most 1 bf16 ulp from bf16(fp64) element-wise.
+* GEMV outputs: max |got - ref| <= 1e-2 * rms(ref) against the unrounded
+  fp64 oracle, measured on the kernel's unrounded fp32 result (mq4_qmm_f32);
+  the bf16 result itself is element-wise at most 1 bf16 ulp from bf16(fp64)
+  or, for outputs near zero where a bf16 ulp is far below fp32 accumulation
+  noise, within 2^-12 * rms(ref).  (Measured against unrounded fp64, bf16
+  output rounding alone costs up to half an ulp of the largest output, about
+  1% of the RMS, so the 1e-2 bar is stated on the fp32 result.)
+* SwiGLU outputs (bf16 op chain): element-wise, see check_swiglu.
 """
 import numpy as np
 import pytest
@@ -27,13 +33,30 @@ def gen_weight(mq4, O, stream_id, N, K, sigma=0.02, dev="cuda:0"):
     return w, to_host_u16(w)
 
 
-def check_close(O, got_bits, ref64, what):
+def rel_err_f32(got_f32, ref64):
+    r = np.asarray(ref64, np.float64)
+    rms = float(np.sqrt(np.mean(r * r)))
+    return float(np.max(np.abs(np.asarray(got_f32, np.float64) - r)) / rms)
+
+
+def check_close(O, got_bits, ref64, what, got_f32=None):
+    """bf16 output: <= 1 ulp of bf16(fp64) (or 2^-12 rms near zero); fp32
+    output (when given): max|err| <= 1e-2 * rms against fp64."""
+    ref64 = np.asarray(ref64, np.float64)
     ref_b = O.f64_to_bf16(ref64)
-    err = O.rel_rms_err(got_bits, ref64)
-    ulp = int(O.bf16_ulp_diff(got_bits, ref_b).max())
-    assert err <= TOL, f"{what}: max|err|/rms = {err:.3e}"
-    assert ulp <= 1, f"{what}: {ulp} bf16 ulps from bf16(fp64)"
-    return err
+    ulp = O.bf16_ulp_diff(got_bits, ref_b)
+    rms = float(np.sqrt(np.mean(ref64 * ref64)))
+    abs_err = np.abs(O.bf16_to_f32(got_bits).astype(np.float64) - ref64)
+    bad = (ulp > 1) & (abs_err > 2.0 ** -12 * rms)
+    msg = (f"{what}: bf16 identical={np.mean(ulp == 0):.4f} max_ulp={int(ulp.max())} "
+           f"bf16 max|err|/rms={O.rel_rms_err(got_bits, ref64):.2e}")
+    if got_f32 is not None:
+        e32 = rel_err_f32(got_f32, ref64)
+        msg += f" fp32 max|err|/rms={e32:.2e}"
+        assert e32 <= TOL, f"{what}: fp32 max|err|/rms = {e32:.3e}"
+    print(msg)
+    assert not bad.any(), f"{what}: {int(bad.sum())} outputs beyond 1 ulp and 2^-12 rms"
+    assert np.mean(ulp == 0) >= 0.98
 
 
 # ---------------------------------------------------------- generator ---
@@ -131,10 +154,14 @@ def test_qmm_matches_fp64_oracle(mq4, O, dev, M, N, K):
     w, wh = gen_weight(mq4, O, 1000 + N % 97, N, K)
     xh = O.gen_normal_bf16(3000 + M, M * K).reshape(M, K)
     qt = mq4.quantize_weight(w)
-    y = mq4.qmatmul(to_dev_bf16(xh, dev), qt)
+    xd = to_dev_bf16(xh, dev)
+    y = mq4.qmatmul(xd, qt)
+    y32 = mq4.quantized_matmul_f32(xd, qt.weight, qt.scales, qt.biases)
     torch.cuda.synchronize()
     ref, _ = O.qmm_f64(xh, *O.quantize(wh))
-    check_close(O, to_host_u16(y), ref, f"qmm {M}x{N}x{K}")
+    check_close(O, to_host_u16(y), ref, f"qmm {M}x{N}x{K}", y32.cpu().numpy())
+    # the bf16 output is the fp32 result rounded once
+    assert np.array_equal(to_host_u16(y), O.f32_to_bf16(y32.cpu().numpy()))
 
 
 def test_qmm_batched_leading_dims(mq4, O, dev):
@@ -149,6 +176,24 @@ def test_qmm_batched_leading_dims(mq4, O, dev):
     check_close(O, to_host_u16(y).reshape(S, N), ref, "qmm [1,S,K]")
 
 
+def check_swiglu(O, got, ref, what):
+    """h is bf16(bf16(bf16(sigmoid(g))*g)*u) of bf16-rounded GEMV outputs g, u.
+    A 1-ulp difference in the rounding of g or u (when the fp32 sum sits next
+    to a bf16 rounding boundary) can flip bf16(sigmoid(g)) by a whole ulp and
+    so move h by several ulps (g = 0.2598 vs 0.2578 gives h = -0.1123 vs
+    -0.1099, 5 ulps).  h is therefore checked element-wise: at least 99%
+    bit-identical, the rest within 8 bf16 ulps or 2^-8 * rms(h) absolute.
+    The 1e-2 RMS bar applies to the GEMV outputs g, u and to the MLP output."""
+    d = O.bf16_ulp_diff(got, ref)
+    rf = O.bf16_to_f32(ref).astype(np.float64)
+    rms = float(np.sqrt(np.mean(rf * rf)))
+    abs_err = np.abs(O.bf16_to_f32(got).astype(np.float64) - rf)
+    print(f"{what}: identical={np.mean(d == 0):.5f} max_ulp={int(d.max())} "
+          f"max|err|/rms={O.rel_rms_err(got, rf):.2e}")
+    assert np.mean(d == 0) >= 0.99
+    assert np.all((d <= 8) | (abs_err <= 2.0 ** -8 * rms))
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 5])
 def test_mlp_gate_up_silu(mq4, O, dev, M):
     N, K = 6144, 2048
@@ -160,21 +205,22 @@ def test_mlp_gate_up_silu(mq4, O, dev, M):
     torch.cuda.synchronize()
     g64, gb = O.qmm_f64(xh, *O.quantize(wgh))
     u64, ub = O.qmm_f64(xh, *O.quantize(wuh))
-    href = O.swiglu_bf16(gb, ub)
-    # reference h from bf16(fp64) g and u; compare within the tolerance
-    err = O.rel_rms_err(to_host_u16(h), O.bf16_to_f32(href).astype(np.float64))
-    assert err <= TOL
-    # the fused kernel equals the unfused ops on its own g and u up to the
-    # rounding of g/u: check against qmm + swiglu from this library
+    check_swiglu(O, to_host_u16(h), O.swiglu_bf16(gb, ub), f"gate_up_silu M={M}")
+    # the unfused ops of this library: g and u meet the GEMV bar, and swiglu
+    # applied to them matches the oracle's swiglu on the same bf16 inputs
     g = mq4.qmatmul(to_dev_bf16(xh, dev), qg)
     u = mq4.qmatmul(to_dev_bf16(xh, dev), qu)
+    xd = to_dev_bf16(xh, dev)
+    check_close(O, to_host_u16(g), g64, "gate",
+                mq4.quantized_matmul_f32(xd, qg.weight, qg.scales, qg.biases).cpu().numpy())
+    check_close(O, to_host_u16(u), u64, "up",
+                mq4.quantized_matmul_f32(xd, qu.weight, qu.scales, qu.biases).cpu().numpy())
     h2 = mq4.swiglu(g, u)
-    d = O.bf16_ulp_diff(to_host_u16(h), to_host_u16(h2))
-    assert d.max() <= 4 and np.mean(d > 0) < 0.01
     # the device expf and libm's may differ in the last float ulp, which can
     # flip a bf16 rounding of sigmoid for a few elements
     d2 = O.bf16_ulp_diff(to_host_u16(h2), O.swiglu_bf16(to_host_u16(g), to_host_u16(u)))
     assert d2.max() <= 2 and np.mean(d2 > 0) < 1e-3
+    check_swiglu(O, to_host_u16(h), to_host_u16(h2), "fused vs unfused")
 
 
 @pytest.mark.parametrize("M", [1, 3])
@@ -196,7 +242,17 @@ def test_qmm_residual_in_place(mq4, O, dev, M):
 
 
 def test_mlp_chain_two_layers(mq4, O, dev):
-    """hidden = hidden + mlp(hidden) twice (src/model/marlin.cpp:142), M=1."""
+    """hidden = hidden + mlp(hidden) for two layers (src/model/marlin.cpp:142),
+    M=1, each step pinned on the GPU's own input to that step:
+      h_l = swiglu(gate x_l, up x_l)   element-wise bar (check_swiglu)
+      y_l = down h_l                   GEMV bar: 1e-2 * rms(y_l) vs fp64
+      x_{l+1} = bf16(x_l + y_l)        bit-exact (same fp32 sum as y_l)
+    The end-to-end stream is then compared with the oracle's own chain.  The
+    bf16 residual stream amplifies ulp-level differences: a 1-ulp change of y
+    flips the rounding of x + y for some elements, whose 1-ulp change (0.4% of
+    the value) in turn flips roundings of the next layer's g and u.  Two
+    correct implementations therefore agree only statistically after a few
+    layers; the end-to-end bar is rms(got - ref) <= 1e-2 * rms(ref)."""
     N, K = 6144, 2048
     layers_d, layers_h = [], []
     for l in range(2):
@@ -205,15 +261,33 @@ def test_mlp_chain_two_layers(mq4, O, dev):
         layers_h.append([O.quantize(h) for _, h in ws])
     xh = O.gen_normal_bf16(3000, K).reshape(1, K)
     x = to_dev_bf16(xh, dev)
-    for lw in layers_d:
-        x = mq4.mlp_forward(x, lw, residual=x)
-    torch.cuda.synchronize()
+    for lw, (g, u, d) in zip(layers_d, layers_h):
+        xin = to_host_u16(x)
+        h = mq4.mlp_gate_up_silu(x, lw.gate_proj, lw.up_proj)
+        y = mq4.qmatmul(h, lw.down_proj)
+        xn = mq4.mlp_forward(x, lw, residual=x)
+        torch.cuda.synchronize()
+        _, gb = O.qmm_f64(xin, *g)
+        _, ub = O.qmm_f64(xin, *u)
+        check_swiglu(O, to_host_u16(h), O.swiglu_bf16(gb, ub), "chain h")
+        y64, _ = O.qmm_f64(to_host_u16(h), *d)
+        y32 = mq4.quantized_matmul_f32(h, lw.down_proj.weight, lw.down_proj.scales, lw.down_proj.biases)
+        check_close(O, to_host_u16(y), y64, "chain down", y32.cpu().numpy())
+        assert np.array_equal(to_host_u16(xn), O.add_bf16(xin, to_host_u16(y)))
+        x = xn
     ref = xh
     for g, u, d in layers_h:
-        _, _, _, y = O.mlp_forward(ref, g, u, d)
-        ref = O.add_bf16(ref, y)
-    err = O.rel_rms_err(to_host_u16(x), O.bf16_to_f32(ref).astype(np.float64))
-    assert err <= TOL
+        _, _, _, yb = O.mlp_forward(ref, g, u, d)
+        ref = O.add_bf16(ref, yb)
+    got = to_host_u16(x)
+    rf = O.bf16_to_f32(ref).astype(np.float64)
+    rms = float(np.sqrt(np.mean(rf * rf)))
+    dd = O.bf16_ulp_diff(got, ref)
+    ae = np.abs(O.bf16_to_f32(got).astype(np.float64) - rf)
+    rel_rms = float(np.sqrt(np.mean(ae * ae))) / rms
+    print(f"chain end: identical={np.mean(dd == 0):.5f} max_ulp={int(dd.max())} "
+          f"max|err|/rms={O.rel_rms_err(got, rf):.2e} rms(err)/rms={rel_rms:.2e}")
+    assert rel_rms <= TOL
 
 
 # ------------------------------------------------------ lm_head/argmax ---
