@@ -28,14 +28,18 @@
  *                        MarlinModel::lm_head (src/model/marlin.cpp:161-169)
  *   mq4_mlp_gate_up_silu swiglu(qmatmul(x, gate), qmatmul(x, up))
  *                        (src/model/marlin.cpp:27-33)
+ *   mq4_rmsnorm_gate_up_silu  the same after rms_norm (src/model/marlin.cpp:141)
  *   mq4_swiglu_bf16      swiglu(gate, up) (src/model/marlin.cpp:27-29)
  *   mq4_qmm_residual     hidden + qmatmul(h, down)
  *                        (src/model/marlin.cpp:34, 142)
  *   mq4_lm_head_argmax   sample_token(lm_head(h)) with temperature <= 0
  *                        (src/model/marlin.cpp:161-169,
  *                        src/sampling/sampler.cpp:9-16)
+ *   mq4_rmsnorm_lm_head_argmax  the same after the final rms_norm
+ *                        (src/model/marlin.cpp:145)
  *   mq4_argmax_bf16      mx::argmax(last_logits, -1)
  *                        (src/sampling/sampler.cpp:15)
+ *   mq4_rms_norm         rms_norm (src/model/marlin.cpp:12-16)
  */
 #ifndef MQ4_H
 #define MQ4_H
@@ -114,24 +118,56 @@ int mq4_mlp_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
                          const uint16_t* up_biases,
                          int64_t N, uint16_t* h, void* stream);
 
+/* The same with the (1 + w) RMSNorm that precedes the MLP fused in front:
+ * xn = bf16(x * rsqrt(mean(x^2) + eps) * (1 + norm_weight)) per row (fp32
+ * math, one rounding), h = swiglu(xn @ Wg^T, xn @ Wu^T).  Replaces
+ * rms_norm(hidden, post_attn_norm) + mlp_forward's gate/up/swiglu
+ * (src/model/marlin.cpp:141, 12-16, 27-33).  norm_weight is bf16 [K],
+ * 16-byte aligned. */
+int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
+                             const uint16_t* norm_weight, float eps,
+                             const uint32_t* gate_wq, const uint16_t* gate_scales,
+                             const uint16_t* gate_biases,
+                             const uint32_t* up_wq, const uint16_t* up_scales,
+                             const uint16_t* up_biases,
+                             int64_t N, uint16_t* h, void* stream);
+
 /* out[i] = bf16(bf16(bf16(sigmoid(gate[i])) * gate[i]) * up[i]): the
  * unfused swiglu (src/model/marlin.cpp:27-29) over n bf16 elements. */
 int mq4_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* out,
                     void* stream);
+
+/* out[m, :] = bf16(x[m, :] * rsqrt(mean(x[m, :]^2) + eps) * (1 + weight)),
+ * computed in fp32 with one rounding: rms_norm with the (1 + w) multiplier
+ * (src/model/marlin.cpp:12-16), the step before the lm_head
+ * (src/model/marlin.cpp:145).  Not a quantized op; provided so a decode step
+ * runs entirely in this library. */
+int mq4_rms_norm(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, float eps,
+                 uint16_t* out, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Greedy lm_head: logits = bf16(h @ W^T) for each of the M rows and
  * idx[m] = argmax over the N bf16 logits of row m, the lowest index winning
  * ties (mx::argmax semantics; src/sampling/sampler.cpp:15).  logits (may be
  * NULL) receives the [M, N] bf16 logits.  workspace is device memory of at
- * least mq4_lm_head_argmax_workspace_size(M, N) bytes, 8-byte aligned; it
- * holds per-block partial results and may be reused by any later call on the
- * same stream. */
+ * least mq4_lm_head_argmax_workspace_size(M, N) bytes, 8-byte aligned, that
+ * holds per-block partial results (no initialisation needed); it may be
+ * reused by later calls on the same stream, and calls that overlap in time
+ * must use different workspaces. */
 size_t mq4_lm_head_argmax_workspace_size(int64_t M, int64_t N);
 int mq4_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K,
                        const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
                        int64_t N, uint32_t* idx, uint16_t* logits,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* The same with the final (1 + w) RMSNorm fused in front
+ * (src/model/marlin.cpp:145, 12-16): logits = bf16(rms_norm(h) @ W^T). */
+int mq4_rmsnorm_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K,
+                               const uint16_t* norm_weight, float eps,
+                               const uint32_t* wq, const uint16_t* scales,
+                               const uint16_t* biases, int64_t N, uint32_t* idx,
+                               uint16_t* logits, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* idx[m] = argmax of row m of bf16 logits [M, N] (lowest index wins ties,
  * NaN never wins over a number).  Same workspace rule as above with

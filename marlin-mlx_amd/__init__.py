@@ -30,7 +30,7 @@ __all__ = [
     "MQ4Error", "library_path", "lib", "QuantizedTensor", "MLPWeights",
     "quantize", "dequantize", "quantized_matmul", "quantized_matmul_f32", "argmax", "swiglu",
     "quantize_weight", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
-    "lm_head", "lm_head_argmax", "sample_token", "fill_normal_bf16",
+    "lm_head", "lm_head_argmax", "sample_token", "rms_norm", "fill_normal_bf16",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -50,7 +50,13 @@ def stream_id_layer(layer: int, proj: int) -> int:
 
 
 STREAM_LM_HEAD = 2000
-STREAM_NORM_WEIGHT = 2001
+STREAM_NORM_WEIGHT = 2001          # final norm (src/model/marlin.cpp:145)
+
+
+def stream_id_layer_norm(layer: int) -> int:
+    """post-attention norm of layer `layer` (src/model/marlin.cpp:141)."""
+    return 2100 + layer
+
 
 
 def stream_id_decode_row(m: int) -> int:
@@ -91,12 +97,15 @@ def lib():
         "mq4_qmm_residual": ([P, I64, I64, P, P, P, I64, P, P, P], I),
         "mq4_qmm_f32": ([P, I64, I64, P, P, P, I64, P, P], I),
         "mq4_mlp_gate_up_silu": ([P, I64, I64, P, P, P, P, P, P, I64, P, P], I),
+        "mq4_rmsnorm_gate_up_silu": ([P, I64, I64, P, ctypes.c_float, P, P, P, P, P, P, I64, P, P], I),
+        "mq4_rmsnorm_lm_head_argmax": ([P, I64, I64, P, ctypes.c_float, P, P, P, I64, P, P, P, SZ, P], I),
         "mq4_swiglu_bf16": ([P, P, I64, P, P], I),
         "mq4_lm_head_argmax_workspace_size": ([I64, I64], SZ),
         "mq4_lm_head_argmax": ([P, I64, I64, P, P, P, I64, P, P, P, SZ, P], I),
         "mq4_argmax_workspace_size": ([I64, I64], SZ),
         "mq4_argmax_bf16": ([P, I64, I64, P, P, SZ, P], I),
         "mq4_fill_normal_bf16": ([P, I64, U64, U64, D, D, I64, P], I),
+        "mq4_rms_norm": ([P, I64, I64, P, ctypes.c_float, P, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -276,8 +285,11 @@ def qmatmul(x: torch.Tensor, w: QuantizedTensor) -> torch.Tensor:
     return quantized_matmul(x, w.weight, w.scales, w.biases, True, w.group_size, w.bits)
 
 
-def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor) -> torch.Tensor:
-    """swiglu(qmatmul(x, gate), qmatmul(x, up)) in one pass over both weights."""
+def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor,
+                     norm_weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
+    """swiglu(qmatmul(x, gate), qmatmul(x, up)) in one pass over both weights;
+    with norm_weight, x is first rms_norm'ed with the (1 + w) multiplier
+    (src/model/marlin.cpp:141) inside the same kernel."""
     _require_quantized(gate, "mlp_gate_up_silu")
     _require_quantized(up, "mlp_gate_up_silu")
     x = _need(x, torch.bfloat16, "x")
@@ -285,9 +297,14 @@ def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor
     if up.out_features != N:
         raise ValueError("mlp_gate_up_silu: gate and up must have the same shape")
     M, K, h = _mk(x, N)
-    _check(lib().mq4_mlp_gate_up_silu(
-        _ptr(x), M, K, _ptr(gate.weight), _ptr(gate.scales), _ptr(gate.biases),
-        _ptr(up.weight), _ptr(up.scales), _ptr(up.biases), N, _ptr(h), _stream(x.device)))
+    g = (_ptr(gate.weight), _ptr(gate.scales), _ptr(gate.biases))
+    u = (_ptr(up.weight), _ptr(up.scales), _ptr(up.biases))
+    if norm_weight is None:
+        _check(lib().mq4_mlp_gate_up_silu(_ptr(x), M, K, *g, *u, N, _ptr(h), _stream(x.device)))
+    else:
+        norm_weight = _need(norm_weight, torch.bfloat16, "norm_weight")
+        _check(lib().mq4_rmsnorm_gate_up_silu(_ptr(x), M, K, _ptr(norm_weight), eps, *g, *u, N, _ptr(h),
+                                              _stream(x.device)))
     return h
 
 
@@ -309,10 +326,12 @@ def qmatmul_residual(x: torch.Tensor, w: QuantizedTensor, residual: torch.Tensor
     return y
 
 
-def mlp_forward(x: torch.Tensor, w: MLPWeights, residual: torch.Tensor | None = None) -> torch.Tensor:
+def mlp_forward(x: torch.Tensor, w: MLPWeights, residual: torch.Tensor | None = None,
+                norm_weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
     """src/model/marlin.cpp:31-35 (down(swiglu(gate x, up x))); with `residual`
-    also the add of src/model/marlin.cpp:142."""
-    h = mlp_gate_up_silu(x, w.gate_proj, w.up_proj)
+    also the add of src/model/marlin.cpp:142, with `norm_weight` the rms_norm
+    of src/model/marlin.cpp:141 in front."""
+    h = mlp_gate_up_silu(x, w.gate_proj, w.up_proj, norm_weight, eps)
     if residual is None:
         return qmatmul(h, w.down_proj)
     return qmatmul_residual(h, w.down_proj, residual)
@@ -323,9 +342,11 @@ def lm_head(hidden: torch.Tensor, w: QuantizedTensor) -> torch.Tensor:
     return qmatmul(hidden, w)
 
 
-def lm_head_argmax(hidden: torch.Tensor, w: QuantizedTensor, return_logits: bool = False):
+def lm_head_argmax(hidden: torch.Tensor, w: QuantizedTensor, return_logits: bool = False,
+                   norm_weight: torch.Tensor | None = None, eps: float = 1e-6):
     """Greedy next token of every row of `hidden`: argmax of the bf16 logits,
-    fused with the lm_head product (marlin.cpp:161-169 + sampler.cpp:14-16)."""
+    fused with the lm_head product (marlin.cpp:161-169 + sampler.cpp:14-16);
+    with norm_weight also the final rms_norm (marlin.cpp:145) in front."""
     _require_quantized(w, "lm_head_argmax")
     hidden = _need(hidden, torch.bfloat16, "hidden")
     N = w.out_features
@@ -336,10 +357,14 @@ def lm_head_argmax(hidden: torch.Tensor, w: QuantizedTensor, return_logits: bool
               if return_logits else None)
     L = lib()
     ws_bytes = L.mq4_lm_head_argmax_workspace_size(M, N)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden.device)
-    _check(L.mq4_lm_head_argmax(_ptr(hidden), M, K, _ptr(w.weight), _ptr(w.scales), _ptr(w.biases),
-                                N, _ptr(idx), _ptr(logits), _ptr(ws), ws_bytes,
-                                _stream(hidden.device)))
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=hidden.device)
+    wargs = (_ptr(w.weight), _ptr(w.scales), _ptr(w.biases), N, _ptr(idx), _ptr(logits), _ptr(ws), ws_bytes,
+             _stream(hidden.device))
+    if norm_weight is None:
+        _check(L.mq4_lm_head_argmax(_ptr(hidden), M, K, *wargs))
+    else:
+        norm_weight = _need(norm_weight, torch.bfloat16, "norm_weight")
+        _check(L.mq4_rmsnorm_lm_head_argmax(_ptr(hidden), M, K, _ptr(norm_weight), eps, *wargs))
     return (idx, logits) if return_logits else idx
 
 
@@ -350,6 +375,17 @@ def sample_token(logits: torch.Tensor, temperature: float = 0.0) -> torch.Tensor
         raise NotImplementedError("sample_token: only greedy (temperature <= 0) sampling is provided")
     last = logits[:, -1, :] if logits.dim() == 3 else logits
     return argmax(last.contiguous(), -1)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """src/model/marlin.cpp:12-16: x * rsqrt(mean(x^2) + eps) * (1 + weight)."""
+    x = _need(x, torch.bfloat16, "x")
+    weight = _need(weight, torch.bfloat16, "weight")
+    K = x.shape[-1]
+    out = torch.empty_like(x)
+    _check(lib().mq4_rms_norm(_ptr(x), x.numel() // K, K, _ptr(weight), eps, _ptr(out),
+                              _stream(x.device)))
+    return out
 
 
 def fill_normal_bf16(shape, stream_id: int, mu: float = 0.0, sigma: float = 1.0,

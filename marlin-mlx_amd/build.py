@@ -23,6 +23,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmq4.so")
+CPP_DEMO_SRC = os.path.join(ROOT, "tests", "cpp", "mq4_cpp_demo.cpp")
+CPP_DEMO = os.path.join(BUILD, "mq4_cpp_demo")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -62,6 +64,13 @@ def build(verbose: bool = True) -> str:
     if p.returncode != 0:
         raise RuntimeError("link failed:\n" + p.stderr)
     os.replace(tmp, LIB)
+    if os.path.exists(CPP_DEMO_SRC):
+        # C++ caller of the header-only host API (tests/cpp), linked to libmq4.so
+        cmd = [HIPCC, "-O2", "-std=c++17", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
+               CPP_DEMO_SRC, "-o", CPP_DEMO, "-L" + HERE, "-lmq4", "-Wl,-rpath,$ORIGIN/.."]
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        if p.returncode != 0:
+            raise RuntimeError("C++ demo build failed:\n" + p.stderr)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
     return LIB

@@ -1,0 +1,180 @@
+// mq4.hpp -- header-only C++ host API over the C ABI of libmq4 (include/mq4.h),
+// mirroring the reference's interface for the quantized path so that a C++
+// caller can replace the MLX ops at the same call sites:
+//
+//   marlin::QuantizedTensor      src/core/types.h:75-82
+//   quantize_weight              src/model/weights.cpp:45-56 (:180-194 lm_head)
+//   qmatmul                      src/model/marlin.cpp:18-25
+//   mlp_forward                  src/model/marlin.cpp:31-35 (+ :141-142)
+//   lm_head                      src/model/marlin.cpp:161-169
+//   sample_token (greedy)        src/sampling/sampler.cpp:9-16
+//
+// Device memory is owned by DeviceBuffer (hipMalloc/hipFree); every call is
+// stream-ordered on the given hipStream_t.  Errors come back as
+// mq4::Result<T> (a value or an Error with the library's message), the
+// C++17 counterpart of the reference's std::expected Result<T>
+// (src/core/types.h:13-19); no exception crosses the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <utility>
+#include <variant>
+
+#include "mq4.h"
+
+namespace mq4 {
+
+struct Error {
+    int code = 0;
+    std::string message;
+};
+
+template <typename T>
+class Result {
+public:
+    Result(T v) : v_(std::move(v)) {}
+    Result(Error e) : v_(std::move(e)) {}
+    bool ok() const { return v_.index() == 0; }
+    explicit operator bool() const { return ok(); }
+    T& value() { return std::get<0>(v_); }
+    const Error& error() const { return std::get<1>(v_); }
+
+private:
+    std::variant<T, Error> v_;
+};
+
+inline Error last_error(int code) { return Error{code, mq4_last_error()}; }
+
+// Owning device allocation.
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t bytes) : bytes_(bytes) {
+        if (bytes && hipMalloc(&p_, bytes) != hipSuccess) {
+            p_ = nullptr;
+            bytes_ = 0;
+        }
+    }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), bytes_(o.bytes_) { o.p_ = nullptr; o.bytes_ = 0; }
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+        if (this != &o) {
+            reset();
+            p_ = o.p_;
+            bytes_ = o.bytes_;
+            o.p_ = nullptr;
+            o.bytes_ = 0;
+        }
+        return *this;
+    }
+    ~DeviceBuffer() { reset(); }
+    void reset() {
+        if (p_) (void)hipFree(p_);
+        p_ = nullptr;
+        bytes_ = 0;
+    }
+    void* get() const { return p_; }
+    size_t bytes() const { return bytes_; }
+    template <typename T>
+    T* as() const { return static_cast<T*>(p_); }
+
+private:
+    void* p_ = nullptr;
+    size_t bytes_ = 0;
+};
+
+// MLX-layout Q4 weight: weight uint32 [N, K/8], scales/biases bf16 [N, K/64].
+struct QuantizedTensor {
+    DeviceBuffer weight, scales, biases;
+    int64_t out_features = 0;   // N
+    int64_t in_features = 0;    // K
+    int group_size = 64;
+    int bits = 4;
+    bool quantized = false;
+
+    const uint32_t* wq() const { return weight.as<uint32_t>(); }
+    const uint16_t* s() const { return scales.as<uint16_t>(); }
+    const uint16_t* b() const { return biases.as<uint16_t>(); }
+};
+
+// quantize_weight (src/model/weights.cpp:45-56): w is a device bf16 [N, K].
+inline Result<QuantizedTensor> quantize_weight(const uint16_t* w, int64_t N, int64_t K,
+                                               hipStream_t stream, int bits = 4, int group_size = 64) {
+    QuantizedTensor q;
+    q.out_features = N;
+    q.in_features = K;
+    q.bits = bits;
+    q.group_size = group_size;
+    q.weight = DeviceBuffer((size_t)N * (size_t)K / 8 * 4);
+    q.scales = DeviceBuffer((size_t)N * (size_t)(K / (group_size > 0 ? group_size : 1)) * 2);
+    q.biases = DeviceBuffer(q.scales.bytes());
+    if (N > 0 && K > 0 && (!q.weight.get() || !q.scales.get() || !q.biases.get()))
+        return Error{MQ4_ERR_HIP, "quantize_weight: device allocation failed"};
+    const int rc = mq4_quantize(w, N, K, group_size, bits, q.weight.as<uint32_t>(), q.scales.as<uint16_t>(),
+                                q.biases.as<uint16_t>(), stream);
+    if (rc != MQ4_OK) return last_error(rc);
+    q.quantized = true;
+    return q;
+}
+
+// qmatmul (src/model/marlin.cpp:18-25): y[M, N] = x[M, K] @ dequant(W)^T.
+inline Result<int> qmatmul(const uint16_t* x, int64_t M, const QuantizedTensor& w, uint16_t* y,
+                           hipStream_t stream) {
+    if (!w.quantized) return Error{MQ4_ERR_UNSUPPORTED, "qmatmul: unquantized weights are outside this library"};
+    const int rc = mq4_qmm(x, M, w.in_features, w.wq(), w.s(), w.b(), w.out_features, 1, w.group_size, w.bits, y,
+                           stream);
+    if (rc != MQ4_OK) return last_error(rc);
+    return 0;
+}
+
+struct MLPWeights {   // src/model/marlin.h:17-21
+    QuantizedTensor gate_proj, up_proj, down_proj;
+};
+
+// hidden = hidden + mlp_forward(rms_norm(hidden, norm_weight)) in two kernels
+// (src/model/marlin.cpp:141-142, 31-35); h is scratch of [M, intermediate].
+inline Result<int> mlp_forward_residual(uint16_t* hidden, int64_t M, const uint16_t* norm_weight, float eps,
+                                        const MLPWeights& w, uint16_t* h, hipStream_t stream) {
+    const int64_t K = w.gate_proj.in_features, N = w.gate_proj.out_features;
+    int rc = norm_weight
+                 ? mq4_rmsnorm_gate_up_silu(hidden, M, K, norm_weight, eps, w.gate_proj.wq(), w.gate_proj.s(),
+                                            w.gate_proj.b(), w.up_proj.wq(), w.up_proj.s(), w.up_proj.b(), N, h,
+                                            stream)
+                 : mq4_mlp_gate_up_silu(hidden, M, K, w.gate_proj.wq(), w.gate_proj.s(), w.gate_proj.b(),
+                                        w.up_proj.wq(), w.up_proj.s(), w.up_proj.b(), N, h, stream);
+    if (rc != MQ4_OK) return last_error(rc);
+    rc = mq4_qmm_residual(h, M, N, w.down_proj.wq(), w.down_proj.s(), w.down_proj.b(), w.down_proj.out_features,
+                          hidden, hidden, stream);
+    if (rc != MQ4_OK) return last_error(rc);
+    return 0;
+}
+
+// Greedy next token(s): idx[m] = argmax(lm_head(rms_norm(hidden))) for each
+// of the M rows (src/model/marlin.cpp:145, 161-169; src/sampling/sampler.cpp:14-16).
+class GreedyLmHead {
+public:
+    GreedyLmHead(int64_t max_rows, int64_t vocab)
+        : ws_(mq4_lm_head_argmax_workspace_size(max_rows, vocab)), max_rows_(max_rows) {}
+    Result<int> operator()(const uint16_t* hidden, int64_t M, const uint16_t* final_norm, float eps,
+                           const QuantizedTensor& lm, uint32_t* idx, uint16_t* logits, hipStream_t stream) {
+        if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "GreedyLmHead: M exceeds max_rows"};
+        const int rc = final_norm
+                           ? mq4_rmsnorm_lm_head_argmax(hidden, M, lm.in_features, final_norm, eps, lm.wq(), lm.s(),
+                                                        lm.b(), lm.out_features, idx, logits, ws_.get(), ws_.bytes(),
+                                                        stream)
+                           : mq4_lm_head_argmax(hidden, M, lm.in_features, lm.wq(), lm.s(), lm.b(),
+                                                lm.out_features, idx, logits, ws_.get(), ws_.bytes(), stream);
+        if (rc != MQ4_OK) return last_error(rc);
+        return 0;
+    }
+
+private:
+    DeviceBuffer ws_;
+    int64_t max_rows_;
+};
+
+}  // namespace mq4

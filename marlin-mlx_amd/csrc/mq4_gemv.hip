@@ -3,26 +3,32 @@
 // Replaces mx::quantized_matmul(x, w, s, b, transpose=true, 64, 4) at the
 // decode call sites: qmatmul (src/model/marlin.cpp:18-25) inside mlp_forward
 // (src/model/marlin.cpp:31-35) and MarlinModel::lm_head
-// (src/model/marlin.cpp:161-169), plus the fusions of the ops around them:
-// swiglu (src/model/marlin.cpp:27-29), the residual add
-// (src/model/marlin.cpp:142) and greedy argmax (src/sampling/sampler.cpp:15).
+// (src/model/marlin.cpp:161-169), plus fusions of the ops around them: the
+// (1 + w) rms_norm before the MLP and before the lm_head
+// (src/model/marlin.cpp:12-16, 141, 145), swiglu (src/model/marlin.cpp:27-29),
+// the residual add (src/model/marlin.cpp:142) and greedy argmax
+// (src/sampling/sampler.cpp:15).
 //
 // Work decomposition (HBM-bound; every weight byte is read exactly once):
 //  * A packed row of K/2 bytes is split into 16-byte slices (4 words = 32 K
 //    elements = half a group).  Lane l of K-split wave kw owns slices
 //    (kw*SPL + j)*64 + l, j < SPL, for every row it visits, so a wave's 16-byte
 //    loads of one row are contiguous (1 KiB per load instruction).
-//  * Because a lane's K range never changes, its activations are loaded once
-//    and kept in registers, pre-paired as bf16x2 to line up with the nibble
-//    pairs (q_p, q_{p+4}) that one AND-OR extracts from a packed word.
-//  * Nibbles become bf16 (128 + q) by OR-ing the exponent bits of 128.0, and
+//  * A lane's K range never changes, so its activations are loaded once and
+//    kept in registers, pre-paired as bf16x2 to line up with the nibble pairs
+//    (q_p, q_{p+4}) that one AND-OR extracts from a packed word.
+//  * Nibbles become bf16 (128 + q) by OR-ing in the exponent bits of 128.0 and
 //    v_dot2_f32_bf16 accumulates x*(128+q) in fp32.  Per half-group the lane
-//    then forms s*D + (b - 128*s)*X with D the dot and X the (precomputed)
-//    sum of its 32 activations, i.e. sum_k x_k*(s*q_k + b) with the bias
-//    factored out of the inner loop (≈11 VALU ops per packed word).
-//  * RPI rows are processed per iteration; the RPI*M (x2 for gate/up) partial
+//    then adds s*D + (b - 128*s)*X, D the dot and X the precomputed sum of its
+//    32 activations: sum_k x_k*(s*q_k + b) with the bias factored out of the
+//    inner loop (about 11 VALU ops per packed word).
+//  * The first batch of weight loads is issued before the activations are
+//    read, so the two memory latencies overlap; with PF the next batch is in
+//    flight while the current one is reduced (streaming kernels).
+//  * RPI rows are processed per round; their RPI*M (x2 for gate/up) partial
 //    sums are reduced across the wave by recursive halving, and across the KS
-//    K-split waves of a block through LDS.
+//    K-split waves of a wave group through LDS.  A block holds NG independent
+//    wave groups.
 #include "mq4_device.h"
 #include "mq4_host.h"
 
@@ -30,10 +36,25 @@ namespace mq4 {
 
 enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3, EPI_STORE_F32 = 4 };
 
+constexpr int kPartialStride = 4096;     // max blocks of an argmax launch
+
 struct QMat {
     const uint32_t* wq;
     const uint16_t* s;
     const uint16_t* b;
+};
+
+struct GemvParams {
+    const uint16_t* x;       // [m_valid, K]
+    int m_valid;
+    int N, K;
+    QMat A, B;               // B: up projection of the fused gate/up kernel
+    uint16_t* y;             // [m_valid, N] (float for EPI_STORE_F32; may be null for ARGMAX)
+    const uint16_t* res;     // EPI_RESIDUAL: [m_valid, N]
+    const uint16_t* norm_w;  // NORM: [K] (1 + w) RMSNorm weight
+    float eps;
+    uint64_t* partial;       // EPI_ARGMAX: [m_valid, kPartialStride] per-block best keys
+    uint32_t* idx;           // EPI_ARGMAX: [m_valid]
 };
 
 // bf16 SwiGLU in MLX's op order: every intermediate is a bf16 tensor.
@@ -46,11 +67,39 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float g_acc, float u_acc) {
     return f32_to_bf16(t * u);
 }
 
-template <int M, int SPL, int RPI, int KS, int EPI>
-__global__ __launch_bounds__(64 * KS) void q4_gemv_kernel(
-    const uint16_t* __restrict__ x, int m_valid, QMat A, QMat B, int N, int K,
-    uint16_t* __restrict__ y, const uint16_t* __restrict__ res, uint64_t* __restrict__ partial,
-    int partial_stride) {
+template <int SPL, int NMAT, int RPI>
+struct WBatch {
+    uint4 w[NMAT][RPI][SPL];
+    uint32_t s[NMAT][RPI][SPL], b[NMAT][RPI][SPL];
+};
+
+// Loads of one row batch.  The addresses are clamped into the matrix (rows to
+// N-1, slices to L-1) so that every load is unconditional: per-lane
+// predicated loads split the load stream into exec-masked branches, which
+// measured about 2.5 us slower per launch on a 14 MB gate/up pass.  The values
+// of clamped lanes are never used: their activations are zero (invalid
+// slices) or their rows are skipped by the epilogue (rows >= N).
+template <int SPL, int NMAT, int RPI>
+__device__ __forceinline__ void load_batch(WBatch<SPL, NMAT, RPI>& W, const QMat& A, const QMat& B, int r0,
+                                           int N, int G, int64_t row_words, const int (&slice)[SPL]) {
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t) {
+        const QMat& Q = (t == 0) ? A : B;
+#pragma unroll
+        for (int r = 0; r < RPI; ++r) {
+            const int row = (r0 + r) < N ? (r0 + r) : (N - 1);
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) {
+                W.w[t][r][j] = load_nt_u4(reinterpret_cast<const uint4*>(Q.wq + (int64_t)row * row_words) + slice[j]);
+                W.s[t][r][j] = Q.s[(int64_t)row * G + (slice[j] >> 1)];
+                W.b[t][r][j] = Q.b[(int64_t)row * G + (slice[j] >> 1)];
+            }
+        }
+    }
+}
+
+template <int M, int SPL, int RPI, int KS, int NG, int EPI, bool PF, bool NORM>
+__global__ __launch_bounds__(64 * KS * NG) void q4_gemv_kernel(GemvParams p) {
     constexpr int NMAT = (EPI == EPI_SWIGLU) ? 2 : 1;
     constexpr int V = NMAT * RPI * M;       // values reduced per row batch
     static_assert(V <= 64, "too many values per wave");
@@ -58,83 +107,150 @@ __global__ __launch_bounds__(64 * KS) void q4_gemv_kernel(
     constexpr int SH = 6 - LOG2V;           // lane >> SH = value index after the wave reduce
 
     const int lane = threadIdx.x & 63;
-    const int kw = threadIdx.x >> 6;
+    const int wid = threadIdx.x >> 6;
+    const int group = wid / KS;
+    const int kw = wid % KS;
+    const int N = p.N, K = p.K, m_valid = p.m_valid;
     const int L = K >> 5;
     const int G = K >> 6;
     const int64_t row_words = K >> 3;
 
-    // ---- activations of this lane's slices, paired for the nibble layout ----
-    uint32_t xp[M][SPL][16];
-    float xs[M][SPL];
-    int slice[SPL];
+    const int n_batches = (N + RPI - 1) / RPI;
+    const int groups_total = gridDim.x * NG;
+    const int gid = blockIdx.x * NG + group;
+    const int rounds = (n_batches + groups_total - 1) / groups_total;   // block-uniform
+
+    int slice[SPL];      // clamped into [0, L) so every load address is valid
     bool valid[SPL];
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-        slice[j] = (kw * SPL + j) * 64 + lane;
-        valid[j] = slice[j] < L;
+        const int sl = (kw * SPL + j) * 64 + lane;
+        valid[j] = sl < L;
+        slice[j] = valid[j] ? sl : (L - 1);
     }
+
+    // ---- first weight batch in flight before the activations are read ----
+    WBatch<SPL, NMAT, RPI> cur;
+    load_batch(cur, p.A, p.B, gid * RPI, N, G, row_words, slice);
+
+    // ---- activations of this lane's slices (optionally RMS-normalized);
+    //      lanes of invalid slices or rows m >= m_valid hold zeros ----
+    uint4 xv[M][SPL][4];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int mm = m < m_valid ? m : (m_valid - 1);
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const bool use = valid[j] && m < m_valid;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint4 v = reinterpret_cast<const uint4*>(p.x + (int64_t)mm * K)[slice[j] * 4 + w];
+                xv[m][j][w] = use ? v : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+    }
+
+    __shared__ float red[NG][(KS > 1) ? KS : 1][(V > M) ? V : M];
+    if (NORM) {
+        // sum of squares of each activation row over all K (this lane's part,
+        // the wave, then the K-split waves of the group)
+        float ss[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < SPL; ++j)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint4 a = xv[m][j][w];
+                    const uint32_t e[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float lo = bf16_to_f32(e[q] & 0xffffu), hi = bf16_to_f32(e[q] >> 16);
+                        s += lo * lo + hi * hi;
+                    }
+                }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+            ss[m] = s;
+        }
+        if (KS > 1) {
+            if (lane == 0)
+#pragma unroll
+                for (int m = 0; m < M; ++m) red[group][kw][m] = ss[m];
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float s = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KS; ++k) s += red[group][k][m];
+                ss[m] = s;
+            }
+            __syncthreads();
+        }
+        // x_k * r * (1 + w_k), one bf16 rounding (src/model/marlin.cpp:12-16)
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            uint4 wn[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) wn[w] = reinterpret_cast<const uint4*>(p.norm_w)[slice[j] * 4 + w];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float r = 1.0f / sqrtf(ss[m] / (float)K + p.eps);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    uint32_t e[4] = {xv[m][j][w].x, xv[m][j][w].y, xv[m][j][w].z, xv[m][j][w].w};
+                    const uint32_t f[4] = {wn[w].x, wn[w].y, wn[w].z, wn[w].w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t lo = f32_to_bf16(bf16_to_f32(e[q] & 0xffffu) * r *
+                                                        (1.0f + bf16_to_f32(f[q] & 0xffffu)));
+                        const uint32_t hi = f32_to_bf16(bf16_to_f32(e[q] >> 16) * r *
+                                                        (1.0f + bf16_to_f32(f[q] >> 16)));
+                        e[q] = lo | (hi << 16);
+                    }
+                    xv[m][j][w] = make_uint4(e[0], e[1], e[2], e[3]);
+                }
+            }
+        }
+    }
+
+    uint32_t xp[M][SPL][16];
+    float xs[M][SPL];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
             float sum = 0.0f;
-            if (valid[j] && m < m_valid) {
-                const uint4* xv = reinterpret_cast<const uint4*>(x + (int64_t)m * K) + slice[j] * 4;
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const uint4 a = xv[w];
-                    xp[m][j][4 * w + 0] = (a.x & 0xffffu) | (a.z << 16);
-                    xp[m][j][4 * w + 1] = (a.x >> 16) | (a.z & 0xffff0000u);
-                    xp[m][j][4 * w + 2] = (a.y & 0xffffu) | (a.w << 16);
-                    xp[m][j][4 * w + 3] = (a.y >> 16) | (a.w & 0xffff0000u);
-                    sum += bf16_to_f32(a.x & 0xffffu) + bf16_to_f32(a.x >> 16) +
-                           bf16_to_f32(a.y & 0xffffu) + bf16_to_f32(a.y >> 16) +
-                           bf16_to_f32(a.z & 0xffffu) + bf16_to_f32(a.z >> 16) +
-                           bf16_to_f32(a.w & 0xffffu) + bf16_to_f32(a.w >> 16);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) xp[m][j][i] = 0u;
+            for (int w = 0; w < 4; ++w) {
+                const uint4 a = xv[m][j][w];
+                xp[m][j][4 * w + 0] = (a.x & 0xffffu) | (a.z << 16);
+                xp[m][j][4 * w + 1] = (a.x >> 16) | (a.z & 0xffff0000u);
+                xp[m][j][4 * w + 2] = (a.y & 0xffffu) | (a.w << 16);
+                xp[m][j][4 * w + 3] = (a.y >> 16) | (a.w & 0xffff0000u);
+                sum += bf16_to_f32(a.x & 0xffffu) + bf16_to_f32(a.x >> 16) + bf16_to_f32(a.y & 0xffffu) +
+                       bf16_to_f32(a.y >> 16) + bf16_to_f32(a.z & 0xffffu) + bf16_to_f32(a.z >> 16) +
+                       bf16_to_f32(a.w & 0xffffu) + bf16_to_f32(a.w >> 16);
             }
             xs[m][j] = sum;
         }
     }
 
-    __shared__ float red[(KS > 1) ? KS : 1][V];
     uint64_t best = 0;   // EPI_ARGMAX: running max key of this lane's value slot
 
-    for (int r0 = blockIdx.x * RPI; r0 < N; r0 += gridDim.x * RPI) {
-        // ---- stream the packed slices of RPI rows (and both matrices) ----
-        uint4 wv[NMAT][RPI][SPL];
-        uint32_t sv[NMAT][RPI][SPL], bv[NMAT][RPI][SPL];
-#pragma unroll
-        for (int t = 0; t < NMAT; ++t) {
-            const QMat& Q = (t == 0) ? A : B;
-#pragma unroll
-            for (int r = 0; r < RPI; ++r) {
-                const int row = r0 + r;
-#pragma unroll
-                for (int j = 0; j < SPL; ++j) {
-                    if (row < N && valid[j]) {
-                        wv[t][r][j] = load_nt_u4(
-                            reinterpret_cast<const uint4*>(Q.wq + (int64_t)row * row_words) + slice[j]);
-                        sv[t][r][j] = Q.s[(int64_t)row * G + (slice[j] >> 1)];
-                        bv[t][r][j] = Q.b[(int64_t)row * G + (slice[j] >> 1)];
-                    } else {
-                        wv[t][r][j] = make_uint4(0u, 0u, 0u, 0u);
-                        sv[t][r][j] = 0u;
-                        bv[t][r][j] = 0u;
-                    }
-                }
-            }
-        }
+    for (int t = 0; t < rounds; ++t) {
+        const int r0 = (t * groups_total + gid) * RPI;
+        WBatch<SPL, NMAT, RPI> nxt;
+        if (PF && t + 1 < rounds)
+            load_batch(nxt, p.A, p.B, ((t + 1) * groups_total + gid) * RPI, N, G, row_words, slice);
 
-        // ---- dot products: value index v = (r*M + m)*NMAT + t ----
+        // ---- dot products: value index v = (r*M + m)*NMAT + mat ----
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 #pragma unroll
-        for (int t = 0; t < NMAT; ++t) {
+        for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll
             for (int r = 0; r < RPI; ++r) {
 #pragma unroll
@@ -142,7 +258,8 @@ __global__ __launch_bounds__(64 * KS) void q4_gemv_kernel(
                     float d[M];
 #pragma unroll
                     for (int m = 0; m < M; ++m) d[m] = 0.0f;
-                    const uint32_t wd[4] = {wv[t][r][j].x, wv[t][r][j].y, wv[t][r][j].z, wv[t][r][j].w};
+                    const uint32_t wd[4] = {cur.w[mt][r][j].x, cur.w[mt][r][j].y, cur.w[mt][r][j].z,
+                                            cur.w[mt][r][j].w};
 #pragma unroll
                     for (int w = 0; w < 4; ++w) {
                         const uint32_t p0 = nib_pair_bf16<0>(wd[w]);
@@ -157,11 +274,10 @@ __global__ __launch_bounds__(64 * KS) void q4_gemv_kernel(
                             d[m] = dot2_bf16(xp[m][j][4 * w + 3], p3, d[m]);
                         }
                     }
-                    const float s = bf16_to_f32(sv[t][r][j]);
-                    const float c = bf16_to_f32(bv[t][r][j]) - 128.0f * s;
+                    const float s = bf16_to_f32(cur.s[mt][r][j]);
+                    const float c = bf16_to_f32(cur.b[mt][r][j]) - 128.0f * s;
 #pragma unroll
-                    for (int m = 0; m < M; ++m)
-                        acc[(r * M + m) * NMAT + t] += s * d[m] + c * xs[m][j];
+                    for (int m = 0; m < M; ++m) acc[(r * M + m) * NMAT + mt] += s * d[m] + c * xs[m][j];
                 }
             }
         }
@@ -170,74 +286,85 @@ __global__ __launch_bounds__(64 * KS) void q4_gemv_kernel(
         float val = wave_multi_reduce<V>(acc, lane);
         int vidx = lane >> SH;                 // value index held by this lane
         bool holder = (lane & ((1 << SH) - 1)) == 0;
+        bool active = true;
         if (KS > 1) {
-            if (holder) red[kw][vidx] = val;
+            if (holder) red[group][kw][vidx] = val;
             __syncthreads();
-            if (kw == 0) {
-                vidx = lane;
-                holder = lane < V;
-                float s = 0.0f;
-                if (holder) {
+            vidx = lane;
+            holder = lane < V;
+            active = kw == 0;
+            float s = 0.0f;
+            if (active && holder) {
 #pragma unroll
-                    for (int k = 0; k < KS; ++k) s += red[k][lane];
-                }
-                val = s;
+                for (int k = 0; k < KS; ++k) s += red[group][k][lane];
             }
+            val = s;
             __syncthreads();
-            if (kw != 0) continue;   // block-uniform loop: all waves still take every iteration
         }
 
         // ---- epilogue ----
-        float other = 0.0f;
-        if (EPI == EPI_SWIGLU) {
-            // the up-projection partner of value index v is v ^ 1
-            const int partner_off = (KS > 1) ? 1 : (1 << SH);
-            other = __shfl_xor(val, partner_off);
+        if (active) {
+            float other = 0.0f;
+            if (EPI == EPI_SWIGLU) {
+                // the up-projection partner of value index v is v ^ 1
+                other = __shfl_xor(val, (KS > 1) ? 1 : (1 << SH));
+            }
+            const int mt = vidx % NMAT;
+            const int m = (vidx / NMAT) % M;
+            const int r = vidx / (NMAT * M);
+            const int row = r0 + r;
+            const bool live = holder && row < N && m < m_valid && (EPI != EPI_SWIGLU || mt == 0);
+            if (EPI == EPI_STORE) {
+                if (live) p.y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16(val);
+            } else if (EPI == EPI_STORE_F32) {
+                if (live) reinterpret_cast<float*>(p.y)[(int64_t)m * N + row] = val;
+            } else if (EPI == EPI_RESIDUAL) {
+                if (live) {
+                    const float rsd = bf16_to_f32(p.res[(int64_t)m * N + row]);
+                    p.y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16(rsd + round_bf16(val));
+                }
+            } else if (EPI == EPI_SWIGLU) {
+                if (live) p.y[(int64_t)m * N + row] = (uint16_t)swiglu_bf16(val, other);
+            } else {  // EPI_ARGMAX
+                const uint32_t lb = f32_to_bf16(val);
+                if (live) {
+                    if (p.y) p.y[(int64_t)m * N + row] = (uint16_t)lb;
+                    const uint64_t key = argmax_key(lb, (uint32_t)row);
+                    best = key > best ? key : best;
+                }
+            }
         }
-        const int t_mat = vidx % NMAT;
-        const int m = (vidx / NMAT) % M;
-        const int r = vidx / (NMAT * M);
-        const int row = r0 + r;
-        const bool live = holder && row < N && m < m_valid && (EPI != EPI_SWIGLU || t_mat == 0);
-        if (EPI == EPI_STORE) {
-            if (live) y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16(val);
-        } else if (EPI == EPI_STORE_F32) {
-            if (live) reinterpret_cast<float*>(y)[(int64_t)m * N + row] = val;
-        } else if (EPI == EPI_RESIDUAL) {
-            if (live) {
-                const float rsd = bf16_to_f32(res[(int64_t)m * N + row]);
-                y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16(rsd + round_bf16(val));
-            }
-        } else if (EPI == EPI_SWIGLU) {
-            if (live) y[(int64_t)m * N + row] = (uint16_t)swiglu_bf16(val, other);
-        } else {  // EPI_ARGMAX
-            const uint32_t lb = f32_to_bf16(val);
-            if (live) {
-                if (y) y[(int64_t)m * N + row] = (uint16_t)lb;
-                const uint64_t key = argmax_key(lb, (uint32_t)row);
-                best = key > best ? key : best;
-            }
+
+        if (t + 1 < rounds) {
+            if (PF) cur = nxt;
+            else load_batch(cur, p.A, p.B, ((t + 1) * groups_total + gid) * RPI, N, G, row_words, slice);
         }
     }
 
     if (EPI == EPI_ARGMAX) {
-        // Only wave 0 carries results when KS > 1.
-        if (KS > 1 && kw != 0) return;
-        // Lane -> m mapping: KS == 1: m = (lane >> SH) % M; KS > 1: m = lane % M.
-        // Max-reduce over every lane bit that does not encode m.
+        // Lane -> m mapping: KS == 1: m = (lane >> SH) % M; KS > 1: m = lane % M
+        // in the group's first wave.  Max-reduce over the lane bits that do not
+        // encode m, then over the groups of the block through LDS.
         const int mshift = (KS > 1) ? 0 : SH;
-        const int mbits = log2_const<M>();
+        constexpr int MB = log2_const<M>();
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const bool is_m_bit = off >= (1 << mshift) && off < (1 << (mshift + mbits));
+            const bool is_m_bit = off >= (1 << mshift) && off < (1 << (mshift + MB));
             if (!is_m_bit) {
                 const uint64_t o = shfl_xor_u64(best, off);
                 best = o > best ? o : best;
             }
         }
-        const int m = (lane >> mshift) & (M - 1);
-        if ((lane & ~((M - 1) << mshift)) == 0 && m < m_valid)
-            partial[(int64_t)m * partial_stride + blockIdx.x] = best;
+        __shared__ uint64_t gbest[NG][M];
+        const int m_of_lane = (lane >> mshift) & (M - 1);
+        if (kw == 0 && (lane & ~((M - 1) << mshift)) == 0) gbest[group][m_of_lane] = best;
+        __syncthreads();
+        if (threadIdx.x < M && (int)threadIdx.x < m_valid) {
+            uint64_t b = gbest[0][threadIdx.x];
+#pragma unroll
+            for (int g = 1; g < NG; ++g) b = gbest[g][threadIdx.x] > b ? gbest[g][threadIdx.x] : b;
+            p.partial[(int64_t)threadIdx.x * kPartialStride + blockIdx.x] = b;
+        }
     }
 }
 
@@ -293,68 +420,122 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
         out[i] = (uint16_t)swiglu_bf16(bf16_to_f32(g[i]), bf16_to_f32(u[i]));
 }
 
+// out[m, :] = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)) per row: the
+// (1 + weight) RMSNorm of src/model/marlin.cpp:12-16, fp32 math, one rounding.
+__global__ __launch_bounds__(256) void rms_norm_1pw_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w, int K,
+                                                           float eps, uint16_t* __restrict__ out) {
+    const uint16_t* xr = x + (int64_t)blockIdx.x * K;
+    uint16_t* orow = out + (int64_t)blockIdx.x * K;
+    float ss = 0.0f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        const float v = bf16_to_f32(xr[k]);
+        ss += v * v;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    __shared__ float part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = part[0] + part[1] + part[2] + part[3];
+    const float r = 1.0f / sqrtf(tot / (float)K + eps);
+    for (int k = threadIdx.x; k < K; k += blockDim.x)
+        orow[k] = (uint16_t)f32_to_bf16(bf16_to_f32(xr[k]) * r * (1.0f + bf16_to_f32(w[k])));
+}
+
 // ------------------------------------------------------------ dispatch ---
 
-constexpr int kMaxGemvBlocks = 4096;     // also the argmax partial stride
 constexpr int kRPI = 4;
 
-struct GemvArgs {
-    const uint16_t* x;
-    int m_valid;
-    QMat A, B;
-    int N, K;
-    uint16_t* y;
-    const uint16_t* res;
-    uint64_t* partial;
-};
+static int g_cus = 0;
+static int num_cus() {
+    if (g_cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_cus = n;
+        else
+            g_cus = 256;
+    }
+    return g_cus;
+}
 
-template <int M, int SPL, int KS, int EPI>
-static void launch_gemv(const GemvArgs& a, hipStream_t st) {
+template <int M, int SPL, int KS, int EPI, bool NORM, int RPI>
+static void launch_single(const GemvParams& a, hipStream_t st) {
+    const int64_t batches = ((int64_t)a.N + RPI - 1) / RPI;
+    hipLaunchKernelGGL((q4_gemv_kernel<M, SPL, RPI, KS, 1, EPI, false, NORM>), dim3((unsigned)batches),
+                       dim3(64 * KS), 0, st, a);
+}
+
+template <int M, int SPL, int KS, int EPI, bool NORM, int RPI>
+static void launch_stream(const GemvParams& a, hipStream_t st) {
+    // Streaming: NG wave groups per block, a grid of a few blocks per CU and
+    // the next batch in flight while the current one is reduced.
+    constexpr int NG = (KS == 1) ? 4 : 1;
+    const int64_t batches = ((int64_t)a.N + RPI - 1) / RPI;
+    int64_t blocks = (batches + NG - 1) / NG;
+    // 4 blocks per CU for the argmax path measured best on a 248320-row
+    // lm_head (2: 61 us, 4: 58 us, 8-16: 60-67 us).
+    const int64_t cap = EPI == EPI_ARGMAX ? (int64_t)num_cus() * 4 : (int64_t)num_cus() * 16 / (KS * NG);
+    if (blocks > cap) blocks = cap;
+    if (blocks > kPartialStride) blocks = kPartialStride;
+    if (blocks < 1) blocks = 1;
+    // Per-block partial keys; a small second kernel reduces them (a last-block
+    // reduction needs a device-scope release fence per block, which measured
+    // three times slower than the extra launch).
+    hipLaunchKernelGGL((q4_gemv_kernel<M, SPL, RPI, KS, NG, EPI, true, NORM>), dim3((unsigned)blocks),
+                       dim3(64 * KS * NG), 0, st, a);
+    if (EPI == EPI_ARGMAX)
+        hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)a.m_valid), dim3(256), 0, st, a.partial,
+                           (int)blocks, kPartialStride, a.idx);
+}
+
+template <int M, int SPL, int KS, int EPI, bool NORM>
+static void launch_gemv(const GemvParams& a, hipStream_t st) {
     constexpr int RPI = (EPI == EPI_SWIGLU && M == 4) ? 2 : kRPI;
-    int64_t batches = ((int64_t)a.N + RPI - 1) / RPI;
-    // About 16 waves per CU at the cap; the argmax partial buffer has one
-    // slot per block, so its grid is capped at the partial stride.
-    int cap = (KS > 1) ? (16 * 256) / KS : kMaxGemvBlocks;
-    if (EPI == EPI_ARGMAX) cap = kMaxGemvBlocks;
-    int grid = (int)(batches < cap ? batches : cap);
-    if (grid < 1) grid = 1;
-    hipLaunchKernelGGL((q4_gemv_kernel<M, SPL, RPI, KS, EPI>), dim3(grid), dim3(64 * KS), 0, st, a.x,
-                       a.m_valid, a.A, a.B, a.N, a.K, a.y, a.res, a.partial, kMaxGemvBlocks);
+    const int64_t batches = ((int64_t)a.N + RPI - 1) / RPI;
+    // RPI 4 measured best for both paths (1 and 2 rows per wave were slower
+    // on the single-pass 6144x2048 gate/up; 8 rows slower when streaming).
+    if (EPI == EPI_ARGMAX || batches > (int64_t)num_cus() * 16 / KS)
+        launch_stream<M, SPL, KS, EPI, NORM, RPI>(a, st);
+    else
+        launch_single<M, SPL, KS, EPI, NORM, RPI>(a, st);
 }
 
 // Pick (SPL, KS) from the number of 16-byte slices per row L = K/32.
-template <int M, int EPI>
-static int dispatch_k(const GemvArgs& a, hipStream_t st) {
+template <int M, int EPI, bool NORM>
+static int dispatch_k(const GemvParams& a, hipStream_t st) {
     const int L = a.K / 32;
-    if (L <= 64) { launch_gemv<M, 1, 1, EPI>(a, st); return 0; }
-    if (L <= 128) { launch_gemv<M, 1, 2, EPI>(a, st); return 0; }
-    if (L <= 192) { launch_gemv<M, 1, 3, EPI>(a, st); return 0; }
-    if (L <= 256) { launch_gemv<M, 1, 4, EPI>(a, st); return 0; }
-    if (L <= 512) { launch_gemv<M, 1, 8, EPI>(a, st); return 0; }
+    if (L <= 64) { launch_gemv<M, 1, 1, EPI, NORM>(a, st); return 0; }
+    if (L <= 128) { launch_gemv<M, 1, 2, EPI, NORM>(a, st); return 0; }
+    if (L <= 192) { launch_gemv<M, 1, 3, EPI, NORM>(a, st); return 0; }
+    if (L <= 256) { launch_gemv<M, 1, 4, EPI, NORM>(a, st); return 0; }
+    if (L <= 512) { launch_gemv<M, 1, 8, EPI, NORM>(a, st); return 0; }
     if constexpr (M == 1) {
-        if (L <= 1024) { launch_gemv<M, 2, 8, EPI>(a, st); return 0; }
-        if (L <= 2048) { launch_gemv<M, 4, 8, EPI>(a, st); return 0; }
+        if (L <= 1024) { launch_gemv<M, 2, 8, EPI, NORM>(a, st); return 0; }
+        if (L <= 2048) { launch_gemv<M, 4, 8, EPI, NORM>(a, st); return 0; }
     }
     return -1;
 }
 
-template <int EPI>
-static int run_gemv(const GemvArgs& base, int M, hipStream_t st) {
+template <int EPI, bool NORM>
+static int run_gemv(const GemvParams& base, int M, hipStream_t st) {
     // Rows of x are processed in chunks of at most 4 (of 1 when K > 16384,
     // where four rows of activations would not fit the register file).
     const int chunk = (base.K / 32 > 512) ? 1 : 4;
     for (int m0 = 0; m0 < M; m0 += chunk) {
-        GemvArgs a = base;
+        GemvParams a = base;
         const int mc = (M - m0) < chunk ? (M - m0) : chunk;
         a.x = base.x + (int64_t)m0 * base.K;
         a.m_valid = mc;
         if (base.y) a.y = base.y + (int64_t)m0 * base.N * (EPI == EPI_STORE_F32 ? 2 : 1);
         if (base.res) a.res = base.res + (int64_t)m0 * base.N;
-        if (base.partial) a.partial = base.partial + (int64_t)m0 * kMaxGemvBlocks;
+        if (base.partial) a.partial = base.partial + (int64_t)m0 * kPartialStride;
+        if (base.idx) a.idx = base.idx + m0;
         int rc;
-        if (mc == 1) rc = dispatch_k<1, EPI>(a, st);
-        else if (mc == 2) rc = dispatch_k<2, EPI>(a, st);
-        else rc = dispatch_k<4, EPI>(a, st);
+        if (mc == 1) rc = dispatch_k<1, EPI, NORM>(a, st);
+        else if (mc == 2) rc = dispatch_k<2, EPI, NORM>(a, st);
+        else rc = dispatch_k<4, EPI, NORM>(a, st);
         if (rc) return rc;
     }
     return 0;
@@ -377,6 +558,70 @@ static int check_qmm_args(const char* what, const uint16_t* x, int64_t M, int64_
     return MQ4_OK;
 }
 
+static int check_norm(const char* what, const uint16_t* norm_w, float eps) {
+    if (!norm_w) return fail(MQ4_ERR_INVALID_ARG, "%s: null norm weight", what);
+    if (!aligned(norm_w, 16)) return fail(MQ4_ERR_ALIGNMENT, "%s: norm weight must be 16-byte aligned", what);
+    if (!(eps >= 0.0f)) return fail(MQ4_ERR_INVALID_ARG, "%s: eps must be >= 0", what);
+    return MQ4_OK;
+}
+
+static GemvParams params(const uint16_t* x, int64_t M, int64_t K, int64_t N, QMat A, QMat B, uint16_t* y) {
+    GemvParams a{};
+    a.x = x;
+    a.m_valid = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.A = A;
+    a.B = B;
+    a.y = y;
+    return a;
+}
+
+template <bool NORM>
+static int gate_up_impl(const char* what, const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_w,
+                        float eps, const uint32_t* gate_wq, const uint16_t* gate_scales,
+                        const uint16_t* gate_biases, const uint32_t* up_wq, const uint16_t* up_scales,
+                        const uint16_t* up_biases, int64_t N, uint16_t* h, void* stream) {
+    if (int rc = check_qmm_args(what, x, M, K, gate_wq, gate_scales, gate_biases, N)) return rc;
+    if (int rc = check_qmm_args(what, x, M, K, up_wq, up_scales, up_biases, N)) return rc;
+    if (NORM)
+        if (int rc = check_norm(what, norm_w, eps)) return rc;
+    if (!h || !aligned(h, 2)) return fail(MQ4_ERR_INVALID_ARG, "%s: h must be a 2-byte aligned pointer", what);
+    GemvParams a = params(x, M, K, N, {gate_wq, gate_scales, gate_biases}, {up_wq, up_scales, up_biases}, h);
+    a.norm_w = norm_w;
+    a.eps = eps;
+    if (run_gemv<EPI_SWIGLU, NORM>(a, (int)M, as_stream(stream)))
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
+    return launch_status(what);
+}
+
+static size_t lm_head_ws_bytes(int64_t M) {
+    return M <= 0 ? 0 : (size_t)M * kPartialStride * sizeof(uint64_t);
+}
+
+template <bool NORM>
+static int lm_head_impl(const char* what, const uint16_t* h, int64_t M, int64_t K, const uint16_t* norm_w,
+                        float eps, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int64_t N,
+                        uint32_t* idx, uint16_t* logits, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+    if (int rc = check_qmm_args(what, h, M, K, wq, scales, biases, N)) return rc;
+    if (NORM)
+        if (int rc = check_norm(what, norm_w, eps)) return rc;
+    if (!idx || !aligned(idx, 4)) return fail(MQ4_ERR_INVALID_ARG, "%s: idx must be a 4-byte aligned pointer", what);
+    if (logits && !aligned(logits, 2)) return fail(MQ4_ERR_ALIGNMENT, "%s: logits must be 2-byte aligned", what);
+    if (!workspace || workspace_bytes < lm_head_ws_bytes(M) || !aligned(workspace, 8))
+        return fail(MQ4_ERR_WORKSPACE, "%s: workspace needs %zu bytes, 8-byte aligned (got %zu)", what,
+                    lm_head_ws_bytes(M), workspace_bytes);
+    GemvParams a = params(h, M, K, N, {wq, scales, biases}, {nullptr, nullptr, nullptr}, logits);
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.partial = reinterpret_cast<uint64_t*>(workspace);
+    a.idx = idx;
+    if (run_gemv<EPI_ARGMAX, NORM>(a, (int)M, as_stream(stream)))
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
+    return launch_status(what);
+}
+
 }  // namespace mq4
 
 using namespace mq4;
@@ -390,9 +635,8 @@ extern "C" int mq4_qmm(const uint16_t* x, int64_t M, int64_t K, const uint32_t* 
         return fail(MQ4_ERR_UNSUPPORTED, "%s: only transpose=1 (x @ W^T) is implemented", what);
     if (int rc = check_qmm_args(what, x, M, K, wq, scales, biases, N)) return rc;
     if (!y || !aligned(y, 2)) return fail(MQ4_ERR_INVALID_ARG, "%s: y must be a 2-byte aligned pointer", what);
-    GemvArgs a{x, (int)M, {wq, scales, biases}, {nullptr, nullptr, nullptr}, (int)N, (int)K, y, nullptr,
-               nullptr};
-    if (run_gemv<EPI_STORE>(a, (int)M, as_stream(stream)))
+    GemvParams a = params(x, M, K, N, {wq, scales, biases}, {nullptr, nullptr, nullptr}, y);
+    if (run_gemv<EPI_STORE, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
@@ -403,9 +647,9 @@ extern "C" int mq4_qmm_f32(const uint16_t* x, int64_t M, int64_t K, const uint32
     const char* what = "mq4_qmm_f32";
     if (int rc = check_qmm_args(what, x, M, K, wq, scales, biases, N)) return rc;
     if (!y || !aligned(y, 4)) return fail(MQ4_ERR_INVALID_ARG, "%s: y must be a 4-byte aligned pointer", what);
-    GemvArgs a{x, (int)M, {wq, scales, biases}, {nullptr, nullptr, nullptr}, (int)N, (int)K,
-               reinterpret_cast<uint16_t*>(y), nullptr, nullptr};
-    if (run_gemv<EPI_STORE_F32>(a, (int)M, as_stream(stream)))
+    GemvParams a = params(x, M, K, N, {wq, scales, biases}, {nullptr, nullptr, nullptr},
+                          reinterpret_cast<uint16_t*>(y));
+    if (run_gemv<EPI_STORE_F32, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
@@ -417,9 +661,9 @@ extern "C" int mq4_qmm_residual(const uint16_t* x, int64_t M, int64_t K, const u
     if (int rc = check_qmm_args(what, x, M, K, wq, scales, biases, N)) return rc;
     if (!y || !residual || !aligned(y, 2) || !aligned(residual, 2))
         return fail(MQ4_ERR_INVALID_ARG, "%s: y and residual must be 2-byte aligned pointers", what);
-    GemvArgs a{x, (int)M, {wq, scales, biases}, {nullptr, nullptr, nullptr}, (int)N, (int)K, y, residual,
-               nullptr};
-    if (run_gemv<EPI_RESIDUAL>(a, (int)M, as_stream(stream)))
+    GemvParams a = params(x, M, K, N, {wq, scales, biases}, {nullptr, nullptr, nullptr}, y);
+    a.res = residual;
+    if (run_gemv<EPI_RESIDUAL, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
@@ -428,45 +672,38 @@ extern "C" int mq4_mlp_gate_up_silu(const uint16_t* x, int64_t M, int64_t K, con
                                     const uint16_t* gate_scales, const uint16_t* gate_biases,
                                     const uint32_t* up_wq, const uint16_t* up_scales,
                                     const uint16_t* up_biases, int64_t N, uint16_t* h, void* stream) {
-    const char* what = "mq4_mlp_gate_up_silu";
-    if (int rc = check_qmm_args(what, x, M, K, gate_wq, gate_scales, gate_biases, N)) return rc;
-    if (int rc = check_qmm_args(what, x, M, K, up_wq, up_scales, up_biases, N)) return rc;
-    if (!h || !aligned(h, 2)) return fail(MQ4_ERR_INVALID_ARG, "%s: h must be a 2-byte aligned pointer", what);
-    GemvArgs a{x, (int)M, {gate_wq, gate_scales, gate_biases}, {up_wq, up_scales, up_biases}, (int)N, (int)K,
-               h, nullptr, nullptr};
-    if (run_gemv<EPI_SWIGLU>(a, (int)M, as_stream(stream)))
-        return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
-    return launch_status(what);
+    return gate_up_impl<false>("mq4_mlp_gate_up_silu", x, M, K, nullptr, 0.0f, gate_wq, gate_scales,
+                               gate_biases, up_wq, up_scales, up_biases, N, h, stream);
+}
+
+extern "C" int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_weight,
+                                        float eps, const uint32_t* gate_wq, const uint16_t* gate_scales,
+                                        const uint16_t* gate_biases, const uint32_t* up_wq,
+                                        const uint16_t* up_scales, const uint16_t* up_biases, int64_t N,
+                                        uint16_t* h, void* stream) {
+    return gate_up_impl<true>("mq4_rmsnorm_gate_up_silu", x, M, K, norm_weight, eps, gate_wq, gate_scales,
+                              gate_biases, up_wq, up_scales, up_biases, N, h, stream);
 }
 
 extern "C" size_t mq4_lm_head_argmax_workspace_size(int64_t M, int64_t N) {
     (void)N;
-    if (M <= 0) return 0;
-    return (size_t)M * kMaxGemvBlocks * sizeof(uint64_t);
+    return lm_head_ws_bytes(M);
 }
 
 extern "C" int mq4_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K, const uint32_t* wq,
                                   const uint16_t* scales, const uint16_t* biases, int64_t N,
                                   uint32_t* idx, uint16_t* logits, void* workspace,
                                   size_t workspace_bytes, void* stream) {
-    const char* what = "mq4_lm_head_argmax";
-    if (int rc = check_qmm_args(what, h, M, K, wq, scales, biases, N)) return rc;
-    if (!idx || !aligned(idx, 4)) return fail(MQ4_ERR_INVALID_ARG, "%s: idx must be a 4-byte aligned pointer", what);
-    if (logits && !aligned(logits, 2)) return fail(MQ4_ERR_ALIGNMENT, "%s: logits must be 2-byte aligned", what);
-    if (!workspace || workspace_bytes < mq4_lm_head_argmax_workspace_size(M, N) || !aligned(workspace, 8))
-        return fail(MQ4_ERR_WORKSPACE, "%s: workspace needs %zu bytes, 8-byte aligned (got %zu)", what,
-                    mq4_lm_head_argmax_workspace_size(M, N), workspace_bytes);
-    uint64_t* partial = reinterpret_cast<uint64_t*>(workspace);
-    GemvArgs a{h, (int)M, {wq, scales, biases}, {nullptr, nullptr, nullptr}, (int)N, (int)K, logits, nullptr,
-               partial};
-    hipStream_t st = as_stream(stream);
-    if (run_gemv<EPI_ARGMAX>(a, (int)M, st)) return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
-    // Every block of the GEMV wrote its partial; blocks = min(row batches, cap).
-    const int64_t batches = (N + kRPI - 1) / kRPI;
-    const int count = (int)(batches < kMaxGemvBlocks ? batches : kMaxGemvBlocks);
-    hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)M), dim3(256), 0, st, partial, count,
-                       kMaxGemvBlocks, idx);
-    return launch_status(what);
+    return lm_head_impl<false>("mq4_lm_head_argmax", h, M, K, nullptr, 0.0f, wq, scales, biases, N, idx, logits,
+                               workspace, workspace_bytes, stream);
+}
+
+extern "C" int mq4_rmsnorm_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K, const uint16_t* norm_weight,
+                                          float eps, const uint32_t* wq, const uint16_t* scales,
+                                          const uint16_t* biases, int64_t N, uint32_t* idx, uint16_t* logits,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+    return lm_head_impl<true>("mq4_rmsnorm_lm_head_argmax", h, M, K, norm_weight, eps, wq, scales, biases, N,
+                              idx, logits, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t mq4_argmax_workspace_size(int64_t M, int64_t N) {
@@ -479,7 +716,7 @@ extern "C" int mq4_argmax_bf16(const uint16_t* logits, int64_t M, int64_t N, uin
                                void* workspace, size_t workspace_bytes, void* stream) {
     const char* what = "mq4_argmax_bf16";
     if (M <= 0 || N <= 0) return fail(MQ4_ERR_INVALID_ARG, "%s: M and N must be positive", what);
-    if (N > 0x7fffffffLL) return fail(MQ4_ERR_UNSUPPORTED, "%s: N too large", what);
+    if (N > 0x7fffffffLL || M > 65535) return fail(MQ4_ERR_UNSUPPORTED, "%s: M or N too large", what);
     if (!logits || !idx) return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
     if (!workspace || workspace_bytes < mq4_argmax_workspace_size(M, N) || !aligned(workspace, 8))
         return fail(MQ4_ERR_WORKSPACE, "%s: workspace needs %zu bytes, 8-byte aligned", what,
@@ -505,5 +742,16 @@ extern "C" int mq4_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int64_t
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), gate, up, n,
                        out);
+    return launch_status(what);
+}
+
+extern "C" int mq4_rms_norm(const uint16_t* x, int64_t M, int64_t K, const uint16_t* weight, float eps,
+                            uint16_t* out, void* stream) {
+    const char* what = "mq4_rms_norm";
+    if (M <= 0 || K <= 0 || M > 0x7fffffffLL || K > 0x7fffffffLL)
+        return fail(MQ4_ERR_INVALID_ARG, "%s: M and K must be positive", what);
+    if (!x || !weight || !out) return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
+    hipLaunchKernelGGL(rms_norm_1pw_kernel, dim3((unsigned)M), dim3(256), 0, as_stream(stream), x, weight,
+                       (int)K, eps, out);
     return launch_status(what);
 }

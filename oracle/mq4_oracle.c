@@ -49,6 +49,7 @@
  * the exact bf16 bit pattern of MLX's sigmoid.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stddef.h>
 #include <string.h>
@@ -361,3 +362,7 @@ void mq4o_rmsnorm_1pw(const uint16_t* x, const uint16_t* w, int64_t M, int64_t K
 void mq4o_add_bf16(const uint16_t* a, const uint16_t* b, int64_t n, uint16_t* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(bf16_to_f32(a[i]) + bf16_to_f32(b[i]));
 }
+
+/* Threads an OpenMP region of this library uses (for reporting the CPU
+ * baseline's core count). */
+int mq4o_omp_threads(void) { return omp_get_max_threads(); }

@@ -53,6 +53,7 @@ def lib():
         L.mq4o_add_bf16.argtypes = [P, P, I64, P]
         L.mq4o_f32_to_bf16_array.argtypes = [P, P, I64]
         L.mq4o_f64_to_bf16_array.argtypes = [P, P, I64]
+        L.mq4o_omp_threads.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -192,6 +193,10 @@ def mlp_forward(x, gate, up, down):
     h = swiglu_bf16(g, u)
     _, y = qmm_f64(h, *down)
     return g, u, h, y
+
+
+def omp_threads() -> int:
+    return int(lib().mq4o_omp_threads())
 
 
 # ---------------------------------------------------- tolerance helpers ---

@@ -1,0 +1,65 @@
+// C++ caller of libmq4 through marlin-mlx_amd/csrc/mq4.hpp, shaped like the
+// reference's decode step (src/model/marlin.cpp:110-145, 161-169): quantize
+// two synthetic layers and an lm_head, run hidden += mlp(rms_norm(hidden))
+// twice, then the greedy lm_head.  Prints the token and the final hidden
+// state's bf16 words so a test can compare them with the Python binding.
+#include <cstdio>
+#include <vector>
+
+#include "mq4.hpp"
+
+#define CHECK(r)                                                                    \
+    do {                                                                            \
+        auto&& r_ = (r);                                                            \
+        if (!r_) {                                                                  \
+            std::fprintf(stderr, "error %d: %s\n", r_.error().code, r_.error().message.c_str()); \
+            return 1;                                                               \
+        }                                                                           \
+    } while (0)
+
+static int fill(uint16_t* p, int64_t n, uint64_t sid, double mu, double sigma, hipStream_t st) {
+    return mq4_fill_normal_bf16(p, n, 0x4D41524Cull, sid, mu, sigma, 0, st);
+}
+
+int main() {
+    const int64_t H = 512, I = 1024, V = 4096, LAYERS = 2;
+    hipStream_t st;
+    if (hipStreamCreate(&st) != hipSuccess) return 2;
+    mq4::DeviceBuffer wtmp(2 * I * H > 2 * V * H ? 2 * I * H : 2 * V * H);
+    std::vector<mq4::MLPWeights> layers(LAYERS);
+    std::vector<mq4::DeviceBuffer> norms;
+    for (int l = 0; l < LAYERS; ++l) {
+        const int64_t shp[3][2] = {{I, H}, {I, H}, {H, I}};
+        mq4::QuantizedTensor* dst[3] = {&layers[l].gate_proj, &layers[l].up_proj, &layers[l].down_proj};
+        for (int p = 0; p < 3; ++p) {
+            if (fill(wtmp.as<uint16_t>(), shp[p][0] * shp[p][1], 1000 + 3 * l + p, 0.0, 0.02, st)) return 3;
+            auto q = mq4::quantize_weight(wtmp.as<uint16_t>(), shp[p][0], shp[p][1], st);
+            CHECK(q);
+            *dst[p] = std::move(q.value());
+        }
+        norms.emplace_back(2 * H);
+        if (fill(norms.back().as<uint16_t>(), H, 2100 + l, 0.1, 0.02, st)) return 3;
+    }
+    if (fill(wtmp.as<uint16_t>(), V * H, 2000, 0.0, 0.02, st)) return 3;
+    auto lmq = mq4::quantize_weight(wtmp.as<uint16_t>(), V, H, st);
+    CHECK(lmq);
+    mq4::DeviceBuffer final_norm(2 * H), hidden(2 * H), h(2 * I), idx(4);
+    if (fill(final_norm.as<uint16_t>(), H, 2001, 0.1, 0.02, st)) return 3;
+    if (fill(hidden.as<uint16_t>(), H, 3000, 0.0, 1.0, st)) return 3;
+    for (int l = 0; l < LAYERS; ++l)
+        CHECK(mq4::mlp_forward_residual(hidden.as<uint16_t>(), 1, norms[l].as<uint16_t>(), 1e-6f, layers[l],
+                                        h.as<uint16_t>(), st));
+    mq4::GreedyLmHead head(1, V);
+    CHECK(head(hidden.as<uint16_t>(), 1, final_norm.as<uint16_t>(), 1e-6f, lmq.value(), idx.as<uint32_t>(), nullptr,
+               st));
+    if (hipStreamSynchronize(st) != hipSuccess) return 4;
+    uint32_t tok = 0;
+    std::vector<uint16_t> hid(H);
+    if (hipMemcpy(&tok, idx.get(), 4, hipMemcpyDeviceToHost) != hipSuccess) return 4;
+    if (hipMemcpy(hid.data(), hidden.get(), 2 * H, hipMemcpyDeviceToHost) != hipSuccess) return 4;
+    std::printf("token %u\nhidden", tok);
+    for (int64_t i = 0; i < H; ++i) std::printf(" %u", hid[i]);
+    std::printf("\n");
+    (void)hipStreamDestroy(st);
+    return 0;
+}

@@ -241,6 +241,70 @@ def test_qmm_residual_in_place(mq4, O, dev, M):
     assert O.rel_rms_err(got, O.bf16_to_f32(ref).astype(np.float64)) <= TOL
 
 
+@pytest.mark.parametrize("M,K", [(1, 2048), (3, 2048), (1, 6144), (2, 128)])
+def test_rmsnorm_gate_up_silu(mq4, O, dev, M, K):
+    """rms_norm(x) (src/model/marlin.cpp:12-16, 141) fused in front of gate/up:
+    h against the oracle's rms_norm -> bf16(fp64 g), bf16(fp64 u) -> swiglu."""
+    N = 1536
+    wg, wgh = gen_weight(mq4, O, 1010, N, K)
+    wu, wuh = gen_weight(mq4, O, 1011, N, K)
+    xh = O.gen_normal_bf16(3000, M * K, 0.0, 1.5).reshape(M, K)
+    nwh = O.gen_normal_bf16(2100, K, 0.1, 0.02)
+    qg, qu = mq4.quantize_weight(wg), mq4.quantize_weight(wu)
+    h = mq4.mlp_gate_up_silu(to_dev_bf16(xh, dev), qg, qu, norm_weight=to_dev_bf16(nwh, dev), eps=1e-6)
+    torch.cuda.synchronize()
+    n = O.rmsnorm_1pw(xh, nwh, 1e-6)
+    _, gb = O.qmm_f64(n, *O.quantize(wgh))
+    _, ub = O.qmm_f64(n, *O.quantize(wuh))
+    check_swiglu(O, to_host_u16(h), O.swiglu_bf16(gb, ub), f"norm+gate_up M={M} K={K}")
+    # the fused norm equals the standalone rms_norm kernel followed by the unfused op
+    n_dev = mq4.rms_norm(to_dev_bf16(xh, dev), to_dev_bf16(nwh, dev), 1e-6)
+    dn = O.bf16_ulp_diff(to_host_u16(n_dev), n)
+    assert dn.max() <= 1 and np.mean(dn > 0) < 1e-3
+    h2 = mq4.mlp_gate_up_silu(n_dev, qg, qu)
+    check_swiglu(O, to_host_u16(h), to_host_u16(h2), "fused norm vs rms_norm kernel")
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_rmsnorm_lm_head_argmax(mq4, O, dev, lm_head, M):
+    qt, (rq, rs, rb) = lm_head
+    xh = O.gen_normal_bf16(3300, M * 2048, 0.0, 3.0).reshape(M, 2048)
+    nwh = O.gen_normal_bf16(2001, 2048, 0.1, 0.02)
+    idx, logits = mq4.lm_head_argmax(to_dev_bf16(xh, dev), qt, return_logits=True,
+                                     norm_weight=to_dev_bf16(nwh, dev), eps=1e-6)
+    torch.cuda.synchronize()
+    hn = O.rmsnorm_1pw(xh, nwh, 1e-6)
+    ref64, refb = O.qmm_f64(hn, rq, rs, rb)
+    lg = to_host_u16(logits)
+    ulp = O.bf16_ulp_diff(lg, refb)
+    print(f"norm+lm_head M={M}: identical={np.mean(ulp == 0):.5f} max_ulp={int(ulp.max())}")
+    assert np.mean(ulp == 0) >= 0.98
+    assert np.array_equal(idx.cpu().numpy().astype(np.uint32), O.argmax_bf16(lg))
+
+
+def test_lm_head_workspace_reuse(mq4, O, dev):
+    """One workspace serves many calls (different shapes and M) in a row."""
+    L = mq4.lib()
+    import ctypes
+    V, K = 50000, 2048
+    w, wh = gen_weight(mq4, O, 2000, V, K)
+    qt = mq4.quantize_weight(w)
+    ws_bytes = L.mq4_lm_head_argmax_workspace_size(5, V)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    P = ctypes.c_void_p
+    for M, Nuse in ((1, V), (5, V), (2, 777), (1, 64), (3, V)):
+        hh = O.gen_normal_bf16(3400 + M, M * K).reshape(M, K)
+        hd = to_dev_bf16(hh, dev)
+        idx = torch.zeros(M, dtype=torch.int32, device=dev)
+        logits = torch.empty((M, Nuse), dtype=torch.bfloat16, device=dev)
+        rc = L.mq4_lm_head_argmax(P(hd.data_ptr()), M, K, P(qt.weight.data_ptr()), P(qt.scales.data_ptr()),
+                                  P(qt.biases.data_ptr()), Nuse, P(idx.data_ptr()), P(logits.data_ptr()),
+                                  P(ws.data_ptr()), ws_bytes, P(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(idx.cpu().numpy().astype(np.uint32), O.argmax_bf16(to_host_u16(logits)))
+
+
 def test_mlp_chain_two_layers(mq4, O, dev):
     """hidden = hidden + mlp(hidden) for two layers (src/model/marlin.cpp:142),
     M=1, each step pinned on the GPU's own input to that step:
