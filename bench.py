@@ -51,6 +51,8 @@ KERNEL_BYTES = {                                  # algorithmic bytes per launch
     "norm_gate_up_silu": 2 * q4_bytes(INTER, HID) + 2 * 2 * HID + 2 * INTER,
     "down_residual": q4_bytes(HID, INTER) + 2 * INTER + 2 * 2 * HID,
     "norm_lm_head_argmax": W_LM + 2 * 2 * HID + 4,
+    # weights + norm weights + x in, token out (activation exchange stays in L2)
+    "decode_step": STEP_BYTES + (LAYERS + 1) * 2 * HID + 2 * HID + 4,
 }
 
 
@@ -250,6 +252,85 @@ def main():
         "traffic": None,
     }
 
+    # ------------------------------------ the whole step in one launch
+    # DecodeStep runs the same step as one persistent kernel (same arithmetic,
+    # so the same token and hidden state as the separate kernels above).
+    qt = lambda q: mq4.QuantizedTensor(q.wq, q.s, q.b)
+    dec_layers = [mq4.DecoderLayer(layer_norms[l], mq4.MLPWeights(qt(g), qt(u), qt(d)))
+                  for l, (g, u, d) in enumerate(layers)]
+    dstep = mq4.DecodeStep(dec_layers, norm_w, qt(lm), EPS)
+    idx_p = torch.zeros((1,), dtype=torch.int32, device=dev)
+    x_p = torch.empty((HID,), dtype=torch.bfloat16, device=dev)
+    run_step(P(torch.cuda.current_stream().cuda_stream))   # x, idx: the separate kernels' result
+    dstep(x0, x_p, idx_p)
+    torch.cuda.synchronize()
+    tok_p = int(idx_p.item())
+    if tok_p != tok_eager or not torch.equal(x_p.view(torch.int16), x.reshape(-1).view(torch.int16)):
+        raise RuntimeError(f"one-launch decode step disagrees with the separate kernels "
+                           f"(token {tok_p} vs {tok_eager})")
+    pgraph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dstep(x0, None, idx_p)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(pgraph):
+        dstep(x0, None, idx_p)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        pgraph.replay()
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(args.steps):
+        pgraph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_step_p = t0.elapsed_time(t1) / args.steps
+    if int(idx_p.item()) != tok_eager:
+        raise RuntimeError("one-launch decode step: graph replay token differs")
+    log(f"[bench] one-launch step {ms_step_p * 1e3:.1f} us, "
+        f"{STEP_BYTES / (ms_step_p * 1e-3) / 1e9:.0f} GB/s")
+    # kernel duration: back-to-back launches between HIP events on the launch stream
+    st = P(torch.cuda.current_stream().cuda_stream)
+    lay_c = dstep._arr
+    dargs = (P(x0.data_ptr()), HID, INTER, LAYERS, ctypes.cast(lay_c, P), P(norm_w.data_ptr()), EPS,
+             *lm.ptrs(), VOCAB, P(idx_p.data_ptr()), None, P(dstep.workspace.data_ptr()), dstep.ws_bytes, st)
+    mq4._check(L.mq4_decode_step(*dargs))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(args.kernel_steps * 5, 10)
+    e0.record()
+    for _ in range(n):
+        L.mq4_decode_step(*dargs)
+    e1.record()
+    torch.cuda.synchronize()
+    mean_us = e0.elapsed_time(e1) * 1e3 / n
+    kernels["decode_step"] = {
+        "mean_us": round(mean_us, 3),
+        "launches_per_step": 1,
+        "us_per_step": round(mean_us, 2),
+        "bytes_per_launch": KERNEL_BYTES["decode_step"],
+        "GBps": round(KERNEL_BYTES["decode_step"] / (mean_us * 1e-6) / 1e9, 1),
+    }
+    log(f"[bench] kernel decode_step: {kernels['decode_step']}")
+    sep = {"us_per_step": round(ms_step * 1e3, 2), "GBps": round(gbps, 1),
+           "note": "the same step as 49 separate kernels (24 x [norm+gate/up+SiLU, down+residual], "
+                   "norm+lm_head+argmax, argmax finalize) replayed from one HIP graph"}
+    if ms_step_p < ms_step:
+        ms_step, gbps = ms_step_p, STEP_BYTES / (ms_step_p * 1e-3) / 1e9
+        dom = "decode_step"
+    dk = kernels[dom]
+    roofline = {
+        "kernel": dom,
+        "bound": "hbm",
+        "achieved": dk["GBps"],
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(dk["GBps"] / HBM_PEAK_GBPS, 4),
+        "traffic": None,
+    }
+
     # ------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu_baseline:
@@ -281,6 +362,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "separate_kernels": sep,
+        "path": "one-launch decode step" if dom == "decode_step" else "separate kernels",
         "pack": {"bytes": pack_bytes, "us": round(pack_ms * 1e3, 1),
                  "GBps": round(pack_bytes / pack_ms / 1e6, 1),
                  "frac": round(pack_bytes / pack_ms / 1e6 / HBM_PEAK_GBPS, 4),

@@ -40,6 +40,9 @@
  *   mq4_argmax_bf16      mx::argmax(last_logits, -1)
  *                        (src/sampling/sampler.cpp:15)
  *   mq4_rms_norm         rms_norm (src/model/marlin.cpp:12-16)
+ *   mq4_decode_step      the per-token MLP + lm_head + greedy token loop body
+ *                        (src/model/marlin.cpp:110-145, 161-169;
+ *                        src/sampling/sampler.cpp:14-16) in one launch
  */
 #ifndef MQ4_H
 #define MQ4_H
@@ -174,6 +177,38 @@ int mq4_rmsnorm_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K,
  * mq4_argmax_workspace_size. */
 size_t mq4_argmax_workspace_size(int64_t M, int64_t N);
 int mq4_argmax_bf16(const uint16_t* logits, int64_t M, int64_t N, uint32_t* idx,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* One whole decode step for one token (M = 1) in a single persistent launch:
+ *   for each layer:  x = x + down(swiglu(gate n, up n)),  n = rms_norm(x, norm)
+ *   idx = argmax(lm_head(rms_norm(x, final_norm)))
+ * i.e. the MLP half of the per-token layer loop (src/model/marlin.cpp:141-142,
+ * 31-35), the final norm (:145), lm_head (:161-169) and greedy sample_token
+ * (src/sampling/sampler.cpp:14-16), with the arithmetic of the separate entry
+ * points above.  Built for hidden = 2048 and intermediate = 6144 (other
+ * shapes return MQ4_ERR_UNSUPPORTED; use the separate entry points), up to
+ * 32 layers, any vocab.  x_out (may be NULL) receives the hidden state after
+ * the last layer.  The launch needs 256 co-resident workgroups, so it must
+ * not overlap other work on the device.  workspace: at least
+ * mq4_decode_workspace_size() bytes, 256-byte aligned, zero-filled once
+ * before first use and then reused by every call on the same stream (calls
+ * that overlap in time need separate workspaces).  If a call ever times out
+ * internally (it cannot when the device runs nothing else), idx receives
+ * 0xFFFFFFFF and every later call with that workspace does the same until
+ * it is zero-filled again. */
+typedef struct mq4_mlp_layer {
+    const uint16_t* norm_weight;                 /* bf16 [hidden] (1 + w) RMSNorm */
+    const uint32_t* gate_wq; const uint16_t* gate_scales; const uint16_t* gate_biases;
+    const uint32_t* up_wq;   const uint16_t* up_scales;   const uint16_t* up_biases;
+    const uint32_t* down_wq; const uint16_t* down_scales; const uint16_t* down_biases;
+} mq4_mlp_layer;
+
+size_t mq4_decode_workspace_size(int64_t hidden, int64_t intermediate, int64_t vocab);
+int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t intermediate, int64_t n_layers,
+                    const mq4_mlp_layer* layers, const uint16_t* final_norm, float eps,
+                    const uint32_t* lm_wq, const uint16_t* lm_scales, const uint16_t* lm_biases,
+                    int64_t vocab, uint32_t* idx, uint16_t* x_out,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------- */

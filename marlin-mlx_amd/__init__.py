@@ -31,6 +31,7 @@ __all__ = [
     "quantize", "dequantize", "quantized_matmul", "quantized_matmul_f32", "argmax", "swiglu",
     "quantize_weight", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
     "lm_head", "lm_head_argmax", "sample_token", "rms_norm", "fill_normal_bf16",
+    "DecoderLayer", "DecodeStep",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -106,6 +107,8 @@ def lib():
         "mq4_argmax_bf16": ([P, I64, I64, P, P, SZ, P], I),
         "mq4_fill_normal_bf16": ([P, I64, U64, U64, D, D, I64, P], I),
         "mq4_rms_norm": ([P, I64, I64, P, ctypes.c_float, P, P], I),
+        "mq4_decode_workspace_size": ([I64, I64, I64], SZ),
+        "mq4_decode_step": ([P, I64, I64, I64, P, P, ctypes.c_float, P, P, P, I64, P, P, P, SZ, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -395,3 +398,83 @@ def fill_normal_bf16(shape, stream_id: int, mu: float = 0.0, sigma: float = 1.0,
     _check(lib().mq4_fill_normal_bf16(_ptr(out), out.numel(), seed, stream_id, mu, sigma, offset,
                                       _stream(out.device)))
     return out
+
+
+# ------------------------------------------------------ whole decode step ---
+
+class _MlpLayerC(ctypes.Structure):
+    """struct mq4_mlp_layer of include/mq4.h."""
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "norm_weight", "gate_wq", "gate_scales", "gate_biases", "up_wq", "up_scales", "up_biases",
+        "down_wq", "down_scales", "down_biases")]
+
+
+@dataclass
+class DecoderLayer:
+    """The MLP half of one decoder layer (src/model/marlin.h:17-21 and the
+    post-attention norm used at src/model/marlin.cpp:141)."""
+    post_attn_norm: torch.Tensor
+    mlp: MLPWeights
+
+
+class DecodeStep:
+    """One greedy decode step for one token in a single launch:
+
+        for layer in layers:  x = x + mlp_forward(rms_norm(x, layer.post_attn_norm))
+        token = argmax(lm_head(rms_norm(x, final_norm)))
+
+    (the MLP half of src/model/marlin.cpp:110-145, then :145, :161-169 and
+    src/sampling/sampler.cpp:14-16).  Same arithmetic as the separate
+    rmsnorm+gate/up, residual-down and rmsnorm+lm_head+argmax entry points, so
+    the token and hidden state are identical to chaining those.  Holds its
+    workspace (zero-filled once here); calls are stream-ordered and must not
+    overlap other device work.  Built for hidden 2048 / intermediate 6144."""
+
+    def __init__(self, layers: list[DecoderLayer], final_norm: torch.Tensor, lm: QuantizedTensor,
+                 eps: float = 1e-6):
+        _require_quantized(lm, "DecodeStep")
+        self.layers = list(layers)
+        self.final_norm = _need(final_norm, torch.bfloat16, "final_norm")
+        self.lm = lm
+        self.eps = float(eps)
+        self.hidden = lm.in_features
+        self.intermediate = self.layers[0].mlp.gate_proj.out_features if self.layers else 6144
+        arr = (_MlpLayerC * max(1, len(self.layers)))()
+        for i, ly in enumerate(self.layers):
+            m = ly.mlp
+            for w in (m.gate_proj, m.up_proj, m.down_proj):
+                _require_quantized(w, "DecodeStep")
+            arr[i] = _MlpLayerC(ly.post_attn_norm.data_ptr(), m.gate_proj.weight.data_ptr(),
+                                m.gate_proj.scales.data_ptr(), m.gate_proj.biases.data_ptr(),
+                                m.up_proj.weight.data_ptr(), m.up_proj.scales.data_ptr(),
+                                m.up_proj.biases.data_ptr(), m.down_proj.weight.data_ptr(),
+                                m.down_proj.scales.data_ptr(), m.down_proj.biases.data_ptr())
+        self._arr = arr
+        L = lib()
+        self.ws_bytes = L.mq4_decode_workspace_size(self.hidden, self.intermediate, lm.out_features)
+        self.workspace = torch.zeros(self.ws_bytes, dtype=torch.uint8, device=self.final_norm.device)
+
+    def reset(self) -> None:
+        """Zero the workspace (clears the sticky error state)."""
+        self.workspace.zero_()
+
+    def __call__(self, x: torch.Tensor, x_out: torch.Tensor | None = None,
+                 idx: torch.Tensor | None = None) -> torch.Tensor:
+        """x: bf16 [hidden] (or [1, hidden]); returns the int32 token tensor [1]
+        (0xFFFFFFFF as int32 -1 after an internal timeout).  x_out, if given,
+        receives the hidden state after the last layer."""
+        x = _need(x, torch.bfloat16, "x")
+        if x.numel() != self.hidden:
+            raise ValueError(f"DecodeStep: x must hold {self.hidden} values (one token)")
+        if idx is None:
+            idx = torch.empty((1,), dtype=torch.int32, device=x.device)
+        if x_out is not None and (x_out.dtype != torch.bfloat16 or x_out.numel() != self.hidden
+                                  or not x_out.is_contiguous()):
+            raise ValueError("DecodeStep: x_out must be a contiguous bf16 tensor of hidden values")
+        lm = self.lm
+        _check(lib().mq4_decode_step(_ptr(x), self.hidden, self.intermediate, len(self.layers),
+                                     ctypes.cast(self._arr, ctypes.c_void_p), _ptr(self.final_norm), self.eps,
+                                     _ptr(lm.weight), _ptr(lm.scales), _ptr(lm.biases), lm.out_features,
+                                     _ptr(idx), _ptr(x_out), _ptr(self.workspace), self.ws_bytes,
+                                     _stream(x.device)))
+        return idx

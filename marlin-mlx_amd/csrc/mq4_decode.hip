@@ -1,0 +1,546 @@
+// Persistent single-launch decode step (M = 1) for gfx950:
+//
+//   for each layer l:  n = rms_norm(x, norm_l);  h = swiglu(n @ Wg^T, n @ Wu^T)
+//                      x = x + h @ Wd^T
+//   token = argmax(rms_norm(x, final_norm) @ Wlm^T)
+//
+// i.e. the per-token loop of src/model/marlin.cpp:110-145 restricted to the
+// MLP half of each layer (rms_norm :141, mlp_forward :31-35, residual :142),
+// then the final norm (:145), lm_head (:161-169) and greedy sample_token
+// (src/sampling/sampler.cpp:14-16), with the same arithmetic as the separate
+// kernels of mq4_gemv.hip.
+//
+// Why one launch: the step is 2 * layers + 1 dependent phases.  Separate
+// kernels drain the memory pipeline at every boundary (every phase pays the
+// full HBM latency); here the weights, which never depend on activations,
+// are loaded one phase ahead into the compute waves' registers, so the HBM
+// stream keeps running while the small activation vectors are exchanged.
+//
+// Exchange without fences or read-modify-write atomics: both measured slow
+// on MI355X (a device-scope release fence writes back the L2; RMW atomics to
+// one address serialize).  Activations travel as 64-bit words, two bf16
+// values in the low half and a 32-bit phase tag in the high half, written
+// and read with relaxed device-scope atomic stores/loads.  A consumer polls
+// the words it needs until every tag equals the phase's tag; each word is
+// self-validating (single-location coherence), so no ordering between
+// different words is needed.  Buffers are rewritten every layer and a phase
+// only overwrites words whose previous contents every consumer has already
+// read (a workgroup can only reach the next write after all workgroups
+// produced the inputs that depended on the previous read).
+//
+// Workgroup roles: 4 I/O waves poll and publish activations and stage them
+// in LDS (pre-paired for the dot2 layout); 8 compute waves hold weights in
+// registers and only touch LDS, so their loads stay in flight across the
+// workgroup barriers (on gfx950 a barrier waits for LDS only, not for
+// outstanding global loads).  Every wait is bounded: on a timeout a sticky
+// error word is set, every workgroup leaves, and the token reads 0xFFFFFFFF.
+#include "mq4_device.h"
+#include "mq4_host.h"
+
+namespace mq4 {
+
+namespace dec {
+
+constexpr int kNWG = 256;            // workgroups (one per CU)
+constexpr int kNIO = 4;              // I/O waves per workgroup
+constexpr int kNCW = 8;              // compute waves per workgroup
+constexpr int kThreads = 64 * (kNIO + kNCW);
+constexpr int kMaxLayers = 32;
+constexpr int H = 2048;              // hidden size this instance is built for
+constexpr int I = 6144;              // intermediate size
+constexpr int SA = H / 32;           // 16-byte slices per gate/up row (64)
+constexpr int SB = I / 32;           // slices per down row (192)
+constexpr int SPL_B = SB / 64;       // down slices per lane (3)
+constexpr int RA = I / kNWG / kNCW;  // gate/up rows per compute wave (3)
+constexpr int RB = H / kNWG / kNCW;  // down rows per compute wave (1)
+constexpr int LM_RPI = 4;            // lm_head rows per batch
+constexpr int LM_NBUF = 3;           // lm_head batches in flight per compute wave
+static_assert(SA == 64 && SB % 64 == 0 && RA * kNWG * kNCW == I && RB * kNWG * kNCW == H, "shape");
+
+struct Layer {
+    const uint16_t* norm;
+    QMat gate, up, down;
+};
+
+struct Params {
+    const uint16_t* x_in;      // [H] bf16
+    uint16_t* x_out;           // [H] bf16 hidden state after the last layer (may be null)
+    uint32_t* idx;             // [1] token
+    const uint16_t* final_norm;
+    float eps;
+    QMat lm;
+    int vocab;
+    int n_layers;
+    uint64_t* xbuf;            // [H/2] tagged words
+    uint64_t* hbuf;            // [I/2] tagged words
+    uint64_t* part;            // [kNWG] tagged per-workgroup argmax keys
+    uint32_t* ctrl;            // [0] epoch, [32] sticky error flag
+    int spin_limit;
+    Layer layers[kMaxLayers];
+};
+
+__device__ __forceinline__ uint64_t ld_tagged(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_tagged(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool errored(const uint32_t* ctrl) {
+    return __hip_atomic_load(ctrl + 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+__device__ __forceinline__ void set_error(uint32_t* ctrl) {
+    __hip_atomic_store(ctrl + 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Poll NW tagged words starting at src (NW a multiple of 64) until every tag
+// equals `tag`; store the 2*NW bf16 values to dst.  false on timeout/abort.
+template <int NW>
+__device__ bool poll_words(const uint64_t* src, uint32_t tag, uint32_t* dst, const Params& p, int lane) {
+    constexpr int PER = NW / 64;
+    uint64_t w[PER];
+    for (int spins = 0;; ++spins) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) w[i] = ld_tagged(src + i * 64 + lane);
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) ok &= (uint32_t)(w[i] >> 32) == tag;
+        if (__all(ok)) break;
+        if (spins >= p.spin_limit || errored(p.ctrl)) {
+            if (lane == 0) set_error(p.ctrl);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dst[i * 64 + lane] = (uint32_t)w[i];
+    return true;
+}
+
+// Pair one slice (16 words = 32 bf16 values) for dot2 and sum its values, in
+// the order of the separate kernels: X = (((0 + c0) + c1) + c2) + c3.
+__device__ __forceinline__ void pair_slice(const uint32_t* words, uint32_t* out16, float* sum) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) s = pair_chunk(reinterpret_cast<const uint4*>(words)[w], out16 + 4 * w, s);
+    *sum = s;
+}
+
+struct alignas(16) Smem {
+    uint32_t xraw[H / 2];          // raw x of the current layer (residual), bf16 pairs
+    uint32_t xp[SA][16];           // dot2-paired normalized x per slice
+    float xs[SA];
+    uint32_t hraw[I / 2];          // h as polled
+    uint32_t hp[SB][16];           // dot2-paired h per slice
+    float hs[SB];
+    uint32_t out[32];              // this workgroup's outputs (bf16 in the low half)
+    uint64_t best[kNCW];
+    uint32_t epoch;
+    int abort;
+};
+
+// dot2 part of one slice: D = sum_k x_k*(128 + q_k) over its 32 elements.
+__device__ __forceinline__ float slice_d(const uint4& w, const uint32_t* xp) {
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    float d = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        d = dot2_bf16(xp[4 * k + 0], nib_pair_bf16<0>(wd[k]), d);
+        d = dot2_bf16(xp[4 * k + 1], nib_pair_bf16<1>(wd[k]), d);
+        d = dot2_bf16(xp[4 * k + 2], nib_pair_bf16<2>(wd[k]), d);
+        d = dot2_bf16(xp[4 * k + 3], nib_pair_bf16<3>(wd[k]), d);
+    }
+    return d;
+}
+
+// Normalize xraw (H bf16) with (1 + w) RMSNorm and build xp/xs.  Every I/O
+// wave computes the full sum of squares (lane l sums the 16 words of slice l,
+// then the wave reduces: the order of the separate kernels) and handles a
+// quarter of the slices, 4 lanes per slice, one 16-byte chunk per lane.
+__device__ void stage_norm_x(Smem& sm, const uint16_t* norm_w, float eps, int io, int lane) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint4 v = reinterpret_cast<const uint4*>(sm.xraw)[lane * 4 + k];
+        ss = sumsq_word(ss, v.x);
+        ss = sumsq_word(ss, v.y);
+        ss = sumsq_word(ss, v.z);
+        ss = sumsq_word(ss, v.w);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    const float r = rms_inv(ss, H, eps);
+    constexpr int SPW = SA / kNIO;                 // 16 slices per I/O wave
+    const int sl = io * SPW + (lane >> 2);
+    const int q = lane & 3;
+    const uint4 nw = reinterpret_cast<const uint4*>(norm_w)[sl * 4 + q];
+    const uint4 xv = reinterpret_cast<const uint4*>(sm.xraw)[sl * 4 + q];
+    const uint4 xn = make_uint4(norm_word(xv.x, nw.x, r), norm_word(xv.y, nw.y, r), norm_word(xv.z, nw.z, r),
+                                norm_word(xv.w, nw.w, r));
+    uint32_t pr[4];
+    const float c = pair_chunk(xn, pr, 0.0f);
+    *reinterpret_cast<uint4*>(&sm.xp[sl][4 * q]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    const float c1 = __shfl_down(c, 1), c2 = __shfl_down(c, 2), c3 = __shfl_down(c, 3);
+    if (q == 0) sm.xs[sl] = ((c + c1) + c2) + c3;
+}
+
+// Pair the polled h (this wave's quarter of the slices).
+__device__ void stage_h(Smem& sm, int io, int lane) {
+    constexpr int SPW = SB / kNIO;    // 48 slices per wave
+    for (int s = lane; s < SPW; s += 64) {
+        const int sl = io * SPW + s;
+        pair_slice(&sm.hraw[sl * 16], sm.hp[sl], &sm.hs[sl]);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
+    __shared__ Smem sm;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wg = blockIdx.x;
+    const int L = p.n_layers;
+
+    if (threadIdx.x == 0) {
+        sm.epoch = __hip_atomic_load(p.ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm.abort = errored(p.ctrl) ? 1 : 0;
+    }
+    __syncthreads();
+    const uint32_t base = sm.epoch * 128u + 1u;  // phase tags base + [0, 2*layers+1]: never 0, disjoint per call
+    if (sm.abort) {
+        if (wg == 0 && threadIdx.x == 0) p.idx[0] = 0xffffffffu;
+        return;
+    }
+
+    if (wave < kNIO) {
+        // ============================ I/O waves ============================
+        const int io = wave;
+        for (int l = 0; l <= L; ++l) {
+            // ---- x of layer l (the input at l == 0) -> xraw ----
+            if (l == 0) {
+#pragma unroll
+                for (int i = 0; i < H / 2 / kNIO / 64; ++i) {
+                    const int word = io * (H / 2 / kNIO) + i * 64 + lane;
+                    const uint32_t v = reinterpret_cast<const uint32_t*>(p.x_in)[word];
+                    sm.xraw[word] = v;
+                    if (L == 0 && wg == 0 && p.x_out) reinterpret_cast<uint32_t*>(p.x_out)[word] = v;
+                }
+            } else if (!poll_words<H / 2 / kNIO>(p.xbuf + io * (H / 2 / kNIO), base + 2 * l,
+                                                 sm.xraw + io * (H / 2 / kNIO), p, lane)) {
+                sm.abort = 1;
+            }
+            __syncthreads();                                   // B1: xraw complete
+            if (sm.abort) break;
+            stage_norm_x(sm, l < L ? p.layers[l].norm : p.final_norm, p.eps, io, lane);
+            __syncthreads();                                   // B2: xp/xs ready
+            if (l == L) break;
+            __syncthreads();                                   // B3: h slice in sm.out
+            if (io == 0 && lane < I / kNWG / 2)
+                st_tagged(p.hbuf + wg * (I / kNWG / 2) + lane,
+                          ((uint64_t)(base + 2 * l + 1) << 32) | (sm.out[2 * lane] | (sm.out[2 * lane + 1] << 16)));
+            if (!poll_words<I / 2 / kNIO>(p.hbuf + io * (I / 2 / kNIO), base + 2 * l + 1,
+                                          sm.hraw + io * (I / 2 / kNIO), p, lane))
+                sm.abort = 1;
+            // the words this wave polled are exactly the slices it pairs
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            stage_h(sm, io, lane);
+            __syncthreads();                                   // B4: hp/hs ready
+            if (sm.abort) break;
+            __syncthreads();                                   // B5: new x rows in sm.out
+            if (io == 0 && lane < H / kNWG / 2) {
+                const uint32_t v = sm.out[2 * lane] | (sm.out[2 * lane + 1] << 16);
+                st_tagged(p.xbuf + wg * (H / kNWG / 2) + lane, ((uint64_t)(base + 2 * l + 2) << 32) | v);
+                if (l == L - 1 && p.x_out)
+                    reinterpret_cast<uint32_t*>(p.x_out)[wg * (H / kNWG / 2) + lane] = v;
+            }
+        }
+        // ---- argmax: this workgroup's best key, then workgroup 0 reduces ----
+        __syncthreads();                                       // B6: sm.best filled
+        const uint32_t tag16 = (sm.epoch % 65535u) + 1u;
+        if (!sm.abort && io == 0) {
+            uint64_t b = lane < kNCW ? sm.best[lane] : 0ull;
+            b = wave_max_u64(b);
+            if (lane == 0) st_tagged(p.part + wg, ((uint64_t)tag16 << 48) | (b & 0xffffffffffffull));
+            if (wg == 0) {
+                uint64_t w[kNWG / 64];
+                bool ok = false;
+                for (int spins = 0;; ++spins) {
+#pragma unroll
+                    for (int i = 0; i < kNWG / 64; ++i) w[i] = ld_tagged(p.part + i * 64 + lane);
+                    bool good = true;
+#pragma unroll
+                    for (int i = 0; i < kNWG / 64; ++i) good &= (uint32_t)(w[i] >> 48) == tag16;
+                    if (__all(good)) { ok = true; break; }
+                    if (spins >= p.spin_limit || errored(p.ctrl)) { if (lane == 0) set_error(p.ctrl); break; }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                uint64_t bb = 0;
+#pragma unroll
+                for (int i = 0; i < kNWG / 64; ++i) {
+                    const uint64_t k = w[i] & 0xffffffffffffull;
+                    bb = k > bb ? k : bb;
+                }
+                bb = wave_max_u64(bb);
+                if (lane == 0) {
+                    p.idx[0] = ok ? argmax_key_index(bb) : 0xffffffffu;
+                    if (ok) __hip_atomic_store(p.ctrl, sm.epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        } else if (sm.abort && wg == 0 && io == 0 && lane == 0) {
+            p.idx[0] = 0xffffffffu;
+        }
+        return;
+    }
+
+    // ============================ compute waves ============================
+    const int cw = wave - kNIO;
+    // weights of the next gate/up and down phases, loaded one phase ahead
+    uint4 wa[2][RA];
+    uint32_t sa[2][RA], ba[2][RA];
+    uint4 wb[RB][SPL_B];
+    uint32_t sb[RB][SPL_B], bb[RB][SPL_B];
+    const int rowA = wg * (I / kNWG) + cw * RA;     // first gate/up row of this wave
+    const int rowB = wg * (H / kNWG) + cw * RB;     // down row of this wave
+
+    auto loadA = [&](int l) {
+        const Layer& Ly = p.layers[l];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const QMat& Q = t == 0 ? Ly.gate : Ly.up;
+#pragma unroll
+            for (int r = 0; r < RA; ++r) {
+                const int row = rowA + r;
+                wa[t][r] = load_nt_u4(reinterpret_cast<const uint4*>(Q.wq + (int64_t)row * (H / 8)) + lane);
+                sa[t][r] = Q.s[row * (H / 64) + (lane >> 1)];
+                ba[t][r] = Q.b[row * (H / 64) + (lane >> 1)];
+            }
+        }
+    };
+    auto loadB = [&](int l) {
+        const QMat& Q = p.layers[l].down;
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < SPL_B; ++j) {
+                const int row = rowB + r, sl = j * 64 + lane;
+                wb[r][j] = load_nt_u4(reinterpret_cast<const uint4*>(Q.wq + (int64_t)row * (I / 8)) + sl);
+                sb[r][j] = Q.s[row * (I / 64) + (sl >> 1)];
+                bb[r][j] = Q.b[row * (I / 64) + (sl >> 1)];
+            }
+    };
+
+    // lm_head streaming state: this wave's batches of LM_RPI rows, LM_NBUF
+    // register buffers so that LM_NBUF - 1 batches are in flight while one is
+    // reduced
+    const int gw = wg * kNCW + cw;
+    const int n_lm_batches = (p.vocab + LM_RPI - 1) / LM_RPI;
+    const int lm_rounds = (n_lm_batches + kNWG * kNCW - 1) / (kNWG * kNCW);
+    struct LmBuf {
+        uint4 w[LM_RPI];
+        uint32_t s[LM_RPI], b[LM_RPI];
+    };
+    LmBuf lb[LM_NBUF];
+    auto loadLM = [&](LmBuf& B, int round) {
+        const int r0 = (round * kNWG * kNCW + gw) * LM_RPI;
+#pragma unroll
+        for (int r = 0; r < LM_RPI; ++r) {
+            const int row = (r0 + r) < p.vocab ? (r0 + r) : (p.vocab - 1);
+            B.w[r] = load_nt_u4(reinterpret_cast<const uint4*>(p.lm.wq + (int64_t)row * (H / 8)) + lane);
+            B.s[r] = p.lm.s[(int64_t)row * (H / 64) + (lane >> 1)];
+            B.b[r] = p.lm.b[(int64_t)row * (H / 64) + (lane >> 1)];
+        }
+    };
+
+    if (L > 0) {
+        loadA(0);
+        loadB(0);
+    }
+    bool aborted = false;
+    for (int l = 0; l < L; ++l) {
+        __syncthreads();                                       // B1
+        if (sm.abort) { aborted = true; break; }
+        __syncthreads();                                       // B2
+        // ---- gate/up rows rowA..rowA+RA-1 ----
+        {
+            uint32_t xp[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xp[i] = sm.xp[lane][i];
+            const float xs = sm.xs[lane];
+            float acc[2 * RA + 2];   // value index v = r*2 + t; padded to 8 values
+#pragma unroll
+            for (int i = 0; i < 2 * RA + 2; ++i) acc[i] = 0.0f;
+#pragma unroll
+            for (int r = 0; r < RA; ++r)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[r * 2 + t] += affine_term(sa[t][r], ba[t][r], slice_d(wa[t][r], xp), xs);
+            const float v = wave_multi_reduce<8>(acc, lane);
+            const float other = __shfl_xor(v, 8);        // up partner of gate value index v^1
+            const int vidx = lane >> 3;
+            if ((lane & 7) == 0 && (vidx & 1) == 0 && (vidx >> 1) < RA)
+                sm.out[cw * RA + (vidx >> 1)] = swiglu_bf16(v, other);
+        }
+        if (l + 1 < L) loadA(l + 1);
+        __syncthreads();                                       // B3
+        __syncthreads();                                       // B4
+        if (sm.abort) { aborted = true; break; }
+        // ---- down row rowB (+ residual) ----
+        {
+            // one partial per 64-slice third of K, reduced over the wave, then
+            // added in order (the K-split order of the separate kernel)
+            static_assert(RB == 1 && SPL_B == 3, "down layout");
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < SPL_B; ++j) {
+                const int sl = j * 64 + lane;
+                uint32_t hp[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) hp[i] = sm.hp[sl][i];
+                acc[j] += affine_term(sb[0][j], bb[0][j], slice_d(wb[0][j], hp), sm.hs[sl]);
+            }
+            const float v = wave_multi_reduce<4>(acc, lane);    // lane >> 4 = third
+            const float v0 = __shfl(v, 0), v1 = __shfl(v, 16), v2 = __shfl(v, 32);
+            float y = 0.0f;
+            y += v0;
+            y += v1;
+            y += v2;
+            if (lane == 0) {
+                const int n = rowB;
+                const uint32_t pair = sm.xraw[n >> 1];
+                const float res = bf16_to_f32((n & 1) ? (pair >> 16) : (pair & 0xffffu));
+                sm.out[cw] = f32_to_bf16(res + round_bf16(y));
+            }
+        }
+        if (l + 1 < L) loadB(l + 1);
+        __syncthreads();                                       // B5
+    }
+
+    // ---- lm_head + argmax over this wave's batches ----
+    // (first two batches issued here, once the layer weights are dead, so they
+    // are in flight during the exchange of the last hidden state)
+    uint64_t best = 0;
+    if (!aborted) {
+#pragma unroll
+        for (int b = 0; b < LM_NBUF; ++b)
+            if (b < lm_rounds) loadLM(lb[b], b);
+        __syncthreads();                                       // B1 (x of the last layer)
+        if (sm.abort) aborted = true;
+    }
+    if (!aborted) {
+        __syncthreads();                                       // B2 (final-normalized x)
+        uint32_t xp[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xp[i] = sm.xp[lane][i];
+        const float xs = sm.xs[lane];
+        auto consume = [&](LmBuf& B, int round) {
+            float acc[LM_RPI];
+#pragma unroll
+            for (int r = 0; r < LM_RPI; ++r) {
+                acc[r] = 0.0f;
+                acc[r] += affine_term(B.s[r], B.b[r], slice_d(B.w[r], xp), xs);
+            }
+            if (round + LM_NBUF < lm_rounds) loadLM(B, round + LM_NBUF);   // refill LM_NBUF rounds ahead
+            const float v = wave_multi_reduce<LM_RPI>(acc, lane);
+            constexpr int SHL = 6 - log2_const<LM_RPI>();
+            const int row = (round * kNWG * kNCW + gw) * LM_RPI + (lane >> SHL);
+            if ((lane & ((1 << SHL) - 1)) == 0 && row < p.vocab) {
+                const uint64_t key = argmax_key(f32_to_bf16(v), (uint32_t)row);
+                best = key > best ? key : best;
+            }
+        };
+        for (int round = 0; round < lm_rounds; round += LM_NBUF) {
+#pragma unroll
+            for (int b = 0; b < LM_NBUF; ++b)
+                if (round + b < lm_rounds) consume(lb[b], round + b);
+        }
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) sm.best[cw] = best;
+    __syncthreads();                                           // B6
+}
+
+}  // namespace dec
+
+static int g_dec_ok = -1;
+
+// Poll iterations before a wait gives up (each iteration is one round trip
+// to L2 plus a short sleep, about 1 us): about a second.
+constexpr int kSpinLimit = 1 << 20;
+
+}  // namespace mq4
+
+using namespace mq4;
+
+extern "C" size_t mq4_decode_workspace_size(int64_t hidden, int64_t intermediate, int64_t vocab) {
+    (void)vocab;
+    if (hidden <= 0 || intermediate <= 0) return 0;
+    // ctrl (256 B) + x words + h words + per-workgroup partial keys, each 256-byte aligned
+    const size_t xw = (size_t)hidden / 2 * 8, hw = (size_t)intermediate / 2 * 8;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    return 256 + up(xw) + up(hw) + up((size_t)dec::kNWG * 8);
+}
+
+extern "C" int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t intermediate, int64_t n_layers,
+                               const mq4_mlp_layer* layers, const uint16_t* final_norm, float eps,
+                               const uint32_t* lm_wq, const uint16_t* lm_scales, const uint16_t* lm_biases,
+                               int64_t vocab, uint32_t* idx, uint16_t* x_out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    const char* what = "mq4_decode_step";
+    if (hidden != dec::H || intermediate != dec::I)
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: built for hidden=%d, intermediate=%d (got %lld, %lld)", what, dec::H,
+                    dec::I, (long long)hidden, (long long)intermediate);
+    if (n_layers < 0 || n_layers > dec::kMaxLayers)
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: n_layers must be in [0, %d]", what, dec::kMaxLayers);
+    if (vocab <= 0 || vocab > (1LL << 30))
+        return fail(MQ4_ERR_INVALID_ARG, "%s: vocab must be in [1, 2^30]", what);
+    if (!x_in || !final_norm || !lm_wq || !lm_scales || !lm_biases || !idx || (n_layers > 0 && !layers))
+        return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
+    if (!aligned(x_in, 16) || !aligned(final_norm, 16) || !aligned(lm_wq, 16) || (x_out && !aligned(x_out, 4)))
+        return fail(MQ4_ERR_ALIGNMENT, "%s: x_in, norms and packed weights must be 16-byte aligned", what);
+    const size_t need = mq4_decode_workspace_size(hidden, intermediate, vocab);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+        return fail(MQ4_ERR_WORKSPACE, "%s: workspace needs %zu bytes, 256-byte aligned, zero-filled once", what,
+                    need);
+    dec::Params p{};
+    for (int64_t l = 0; l < n_layers; ++l) {
+        const mq4_mlp_layer& s = layers[l];
+        if (!s.norm_weight || !s.gate_wq || !s.gate_scales || !s.gate_biases || !s.up_wq || !s.up_scales ||
+            !s.up_biases || !s.down_wq || !s.down_scales || !s.down_biases)
+            return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer in layer %lld", what, (long long)l);
+        if (!aligned(s.norm_weight, 16) || !aligned(s.gate_wq, 16) || !aligned(s.up_wq, 16) ||
+            !aligned(s.down_wq, 16))
+            return fail(MQ4_ERR_ALIGNMENT, "%s: layer %lld pointers must be 16-byte aligned", what, (long long)l);
+        p.layers[l] = {s.norm_weight,
+                       {s.gate_wq, s.gate_scales, s.gate_biases},
+                       {s.up_wq, s.up_scales, s.up_biases},
+                       {s.down_wq, s.down_scales, s.down_biases}};
+    }
+    if (g_dec_ok < 0) {
+        int dev = 0, cus = 0, occ = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, dec::decode_step_kernel, dec::kThreads, 0) !=
+                hipSuccess)
+            return fail(MQ4_ERR_HIP, "%s: device query failed", what);
+        g_dec_ok = (cus >= dec::kNWG && occ >= 1) ? 1 : 0;
+    }
+    if (g_dec_ok == 0)
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: needs %d co-resident workgroups of %d threads", what, dec::kNWG,
+                    dec::kThreads);
+    p.x_in = x_in;
+    p.x_out = x_out;
+    p.idx = idx;
+    p.final_norm = final_norm;
+    p.eps = eps;
+    p.lm = {lm_wq, lm_scales, lm_biases};
+    p.vocab = (int)vocab;
+    p.n_layers = (int)n_layers;
+    char* ws = reinterpret_cast<char*>(workspace);
+    const size_t xw = ((size_t)hidden / 2 * 8 + 255) / 256 * 256, hw = ((size_t)intermediate / 2 * 8 + 255) / 256 * 256;
+    p.ctrl = reinterpret_cast<uint32_t*>(ws);
+    p.xbuf = reinterpret_cast<uint64_t*>(ws + 256);
+    p.hbuf = reinterpret_cast<uint64_t*>(ws + 256 + xw);
+    p.part = reinterpret_cast<uint64_t*>(ws + 256 + xw + hw);
+    p.spin_limit = kSpinLimit;
+    hipLaunchKernelGGL(dec::decode_step_kernel, dim3(dec::kNWG), dim3(dec::kThreads), 0, as_stream(stream), p);
+    return launch_status(what);
+}

@@ -10,6 +10,13 @@ constexpr int kWave = 64;     // CDNA wavefront width
 constexpr int kGroup = 64;    // MLX affine group size along K
 constexpr int kSlice = 32;    // K elements per 16-byte packed slice (4 words)
 
+// One MLX-layout Q4 matrix: packed words [N, K/8], bf16 scales/biases [N, K/64].
+struct QMat {
+    const uint32_t* wq;
+    const uint16_t* s;
+    const uint16_t* b;
+};
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -45,6 +52,70 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 template <int P>
 __device__ __forceinline__ uint32_t nib_pair_bf16(uint32_t word) {
     return ((word >> (4 * P)) & 0x000F000Fu) | 0x43004300u;
+}
+
+// ---- per-element arithmetic shared by every decode kernel ----
+// The separate kernels (mq4_gemv.hip) and the persistent decode step
+// (mq4_decode.hip) call these same functions in the same order, so the two
+// paths produce bit-identical results.  FP contraction is off inside them and
+// every fused multiply-add is written out, so the compiler cannot fuse
+// differently in different kernels.
+
+// Contribution of one 16-byte slice (32 K elements, half a group):
+// sum_k x_k*(s*q_k + b) = s*D + (b - 128*s)*X with D = sum_k x_k*(128 + q_k)
+// (the dot2 of the nibble pairs) and X = sum_k x_k.
+__device__ __forceinline__ float affine_term(uint32_t sbits, uint32_t bbits, float d, float xsum) {
+#pragma clang fp contract(off)
+    const float s = bf16_to_f32(sbits);
+    const float c = bf16_to_f32(bbits) - 128.0f * s;    // 128*s is exact
+    return __builtin_fmaf(s, d, c * xsum);
+}
+
+// s + lo^2 + hi^2 of one word holding two bf16 values.
+__device__ __forceinline__ float sumsq_word(float s, uint32_t v) {
+#pragma clang fp contract(off)
+    const float lo = bf16_to_f32(v & 0xffffu), hi = bf16_to_f32(v >> 16);
+    return s + __builtin_fmaf(lo, lo, hi * hi);
+}
+
+// 1 / sqrt(mean(x^2) + eps) from the fp32 sum of squares of K values.
+__device__ __forceinline__ float rms_inv(float ss, int K, float eps) {
+#pragma clang fp contract(off)
+    return 1.0f / sqrtf(ss / (float)K + eps);
+}
+
+// (1 + w) RMSNorm of one word of two bf16 values, one bf16 rounding each
+// (src/model/marlin.cpp:12-16).
+__device__ __forceinline__ uint32_t norm_word(uint32_t x, uint32_t w, float r) {
+#pragma clang fp contract(off)
+    const uint32_t lo = f32_to_bf16(bf16_to_f32(x & 0xffffu) * r * (1.0f + bf16_to_f32(w & 0xffffu)));
+    const uint32_t hi = f32_to_bf16(bf16_to_f32(x >> 16) * r * (1.0f + bf16_to_f32(w >> 16)));
+    return lo | (hi << 16);
+}
+
+// One 16-byte activation chunk (8 bf16 values in words a.x..a.w) -> the four
+// dot2 pairs (v_p, v_{p+4}) matching nib_pair_bf16<0..3> of one packed word,
+// and sum + (the 8 values, left to right).
+__device__ __forceinline__ float pair_chunk(const uint4& a, uint32_t* out4, float sum) {
+#pragma clang fp contract(off)
+    out4[0] = (a.x & 0xffffu) | (a.z << 16);
+    out4[1] = (a.x >> 16) | (a.z & 0xffff0000u);
+    out4[2] = (a.y & 0xffffu) | (a.w << 16);
+    out4[3] = (a.y >> 16) | (a.w & 0xffff0000u);
+    return sum + (bf16_to_f32(a.x & 0xffffu) + bf16_to_f32(a.x >> 16) + bf16_to_f32(a.y & 0xffffu) +
+                  bf16_to_f32(a.y >> 16) + bf16_to_f32(a.z & 0xffffu) + bf16_to_f32(a.z >> 16) +
+                  bf16_to_f32(a.w & 0xffffu) + bf16_to_f32(a.w >> 16));
+}
+
+// bf16 SwiGLU in MLX's op order (src/model/marlin.cpp:27-29): every
+// intermediate is a bf16 tensor.
+__device__ __forceinline__ uint32_t swiglu_bf16(float g_acc, float u_acc) {
+#pragma clang fp contract(off)
+    const float g = round_bf16(g_acc);
+    const float u = round_bf16(u_acc);
+    const float sg = round_bf16(1.0f / (1.0f + expf(-g)));
+    const float t = round_bf16(sg * g);
+    return f32_to_bf16(t * u);
 }
 
 // Monotone 16-bit key of a bf16 value for max-selection: larger value ->
@@ -97,8 +168,11 @@ __device__ __forceinline__ float wave_multi_reduce(float (&v)[V], int lane) {
 #pragma unroll
             for (int i = 0; i < V / 2; ++i) {
                 if (i < h) {
-                    float send = upper ? v[i] : v[i + h];
-                    float keep = upper ? v[i + h] : v[i];
+                    // both values read first: a select between two array
+                    // elements would keep v[] in memory instead of registers
+                    const float lo = v[i], hi = v[i + h];
+                    const float send = upper ? lo : hi;
+                    const float keep = upper ? hi : lo;
                     v[i] = keep + __shfl_xor(send, off);
                 }
             }

@@ -38,12 +38,6 @@ enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3,
 
 constexpr int kPartialStride = 4096;     // max blocks of an argmax launch
 
-struct QMat {
-    const uint32_t* wq;
-    const uint16_t* s;
-    const uint16_t* b;
-};
-
 struct GemvParams {
     const uint16_t* x;       // [m_valid, K]
     int m_valid;
@@ -56,16 +50,6 @@ struct GemvParams {
     uint64_t* partial;       // EPI_ARGMAX: [m_valid, kPartialStride] per-block best keys
     uint32_t* idx;           // EPI_ARGMAX: [m_valid]
 };
-
-// bf16 SwiGLU in MLX's op order: every intermediate is a bf16 tensor.
-__device__ __forceinline__ uint32_t swiglu_bf16(float g_acc, float u_acc) {
-#pragma clang fp contract(off)
-    const float g = round_bf16(g_acc);
-    const float u = round_bf16(u_acc);
-    const float sg = round_bf16(1.0f / (1.0f + expf(-g)));
-    const float t = round_bf16(sg * g);
-    return f32_to_bf16(t * u);
-}
 
 template <int SPL, int NMAT, int RPI>
 struct WBatch {
@@ -165,10 +149,7 @@ __global__ __launch_bounds__(64 * KS * NG) void q4_gemv_kernel(GemvParams p) {
                     const uint4 a = xv[m][j][w];
                     const uint32_t e[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float lo = bf16_to_f32(e[q] & 0xffffu), hi = bf16_to_f32(e[q] >> 16);
-                        s += lo * lo + hi * hi;
-                    }
+                    for (int q = 0; q < 4; ++q) s = sumsq_word(s, e[q]);
                 }
 #pragma unroll
             for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
@@ -196,20 +177,12 @@ __global__ __launch_bounds__(64 * KS * NG) void q4_gemv_kernel(GemvParams p) {
             for (int w = 0; w < 4; ++w) wn[w] = reinterpret_cast<const uint4*>(p.norm_w)[slice[j] * 4 + w];
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float r = 1.0f / sqrtf(ss[m] / (float)K + p.eps);
+                const float r = rms_inv(ss[m], K, p.eps);
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    uint32_t e[4] = {xv[m][j][w].x, xv[m][j][w].y, xv[m][j][w].z, xv[m][j][w].w};
-                    const uint32_t f[4] = {wn[w].x, wn[w].y, wn[w].z, wn[w].w};
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint32_t lo = f32_to_bf16(bf16_to_f32(e[q] & 0xffffu) * r *
-                                                        (1.0f + bf16_to_f32(f[q] & 0xffffu)));
-                        const uint32_t hi = f32_to_bf16(bf16_to_f32(e[q] >> 16) * r *
-                                                        (1.0f + bf16_to_f32(f[q] >> 16)));
-                        e[q] = lo | (hi << 16);
-                    }
-                    xv[m][j][w] = make_uint4(e[0], e[1], e[2], e[3]);
+                    const uint4 e = xv[m][j][w];
+                    xv[m][j][w] = make_uint4(norm_word(e.x, wn[w].x, r), norm_word(e.y, wn[w].y, r),
+                                             norm_word(e.z, wn[w].z, r), norm_word(e.w, wn[w].w, r));
                 }
             }
         }
@@ -223,16 +196,7 @@ __global__ __launch_bounds__(64 * KS * NG) void q4_gemv_kernel(GemvParams p) {
         for (int j = 0; j < SPL; ++j) {
             float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint4 a = xv[m][j][w];
-                xp[m][j][4 * w + 0] = (a.x & 0xffffu) | (a.z << 16);
-                xp[m][j][4 * w + 1] = (a.x >> 16) | (a.z & 0xffff0000u);
-                xp[m][j][4 * w + 2] = (a.y & 0xffffu) | (a.w << 16);
-                xp[m][j][4 * w + 3] = (a.y >> 16) | (a.w & 0xffff0000u);
-                sum += bf16_to_f32(a.x & 0xffffu) + bf16_to_f32(a.x >> 16) + bf16_to_f32(a.y & 0xffffu) +
-                       bf16_to_f32(a.y >> 16) + bf16_to_f32(a.z & 0xffffu) + bf16_to_f32(a.z >> 16) +
-                       bf16_to_f32(a.w & 0xffffu) + bf16_to_f32(a.w >> 16);
-            }
+            for (int w = 0; w < 4; ++w) sum = pair_chunk(xv[m][j][w], &xp[m][j][4 * w], sum);
             xs[m][j] = sum;
         }
     }
@@ -274,10 +238,9 @@ __global__ __launch_bounds__(64 * KS * NG) void q4_gemv_kernel(GemvParams p) {
                             d[m] = dot2_bf16(xp[m][j][4 * w + 3], p3, d[m]);
                         }
                     }
-                    const float s = bf16_to_f32(cur.s[mt][r][j]);
-                    const float c = bf16_to_f32(cur.b[mt][r][j]) - 128.0f * s;
 #pragma unroll
-                    for (int m = 0; m < M; ++m) acc[(r * M + m) * NMAT + mt] += s * d[m] + c * xs[m][j];
+                    for (int m = 0; m < M; ++m)
+                        acc[(r * M + m) * NMAT + mt] += affine_term(cur.s[mt][r][j], cur.b[mt][r][j], d[m], xs[m][j]);
                 }
             }
         }
@@ -438,7 +401,7 @@ __global__ __launch_bounds__(256) void rms_norm_1pw_kernel(const uint16_t* __res
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
     __syncthreads();
     const float tot = part[0] + part[1] + part[2] + part[3];
-    const float r = 1.0f / sqrtf(tot / (float)K + eps);
+    const float r = rms_inv(tot, K, eps);
     for (int k = threadIdx.x; k < K; k += blockDim.x)
         orow[k] = (uint16_t)f32_to_bf16(bf16_to_f32(xr[k]) * r * (1.0f + bf16_to_f32(w[k])));
 }

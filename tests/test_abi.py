@@ -107,3 +107,47 @@ def test_python_api_rejects_host_tensors(mq4):
         mq4.quantize(torch.zeros(4, 64, dtype=torch.float32))
     with pytest.raises(NotImplementedError):
         mq4.sample_token(torch.zeros(1, 1, 8, dtype=torch.bfloat16), temperature=0.7)
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "norm_weight", "gate_wq", "gate_scales", "gate_biases", "up_wq", "up_scales", "up_biases",
+        "down_wq", "down_scales", "down_biases")]
+
+
+def test_decode_step_validation(mq4):
+    """Every rejection of mq4_decode_step happens before its first HIP call."""
+    L = mq4.lib()
+    need = L.mq4_decode_workspace_size(2048, 6144, 248320)
+    assert need > 0 and need % 256 == 0
+    good = _Layer(*([A16] * 10))
+    arr = (_Layer * 2)(good, good)
+
+    def call(**kw):
+        return L.mq4_decode_step(
+            kw.get("x", fake(A16)), kw.get("hidden", 2048), kw.get("inter", 6144), kw.get("n", 2),
+            kw.get("layers", ctypes.cast(arr, ctypes.c_void_p)), kw.get("fn", fake(A16)), 1e-6,
+            kw.get("wq", fake(A16)), fake(A16), fake(A16), kw.get("vocab", 248320), kw.get("idx", fake(A16)),
+            kw.get("xo", None), kw.get("ws", fake(0x200000)), kw.get("wsb", need), S)
+
+    assert call(hidden=4096) == UNSUPPORTED
+    assert "hidden" in last_error(mq4)
+    assert call(inter=8192) == UNSUPPORTED
+    assert call(n=33) == UNSUPPORTED
+    assert call(n=-1) == UNSUPPORTED
+    assert call(vocab=0) == INVALID
+    assert call(vocab=(1 << 30) + 1) == INVALID
+    assert call(x=None) == INVALID
+    assert call(idx=None) == INVALID
+    assert call(layers=None) == INVALID
+    assert call(x=fake(A16 + 2)) == ALIGN
+    assert call(wq=fake(A16 + 4)) == ALIGN
+    assert call(xo=fake(A16 + 2)) == ALIGN
+    assert call(ws=None) == WORKSPACE
+    assert call(wsb=need - 1) == WORKSPACE
+    assert call(ws=fake(0x200000 + 128)) == WORKSPACE
+    bad = (_Layer * 2)(good, _Layer(*([A16] * 9 + [0])))
+    assert call(layers=ctypes.cast(bad, ctypes.c_void_p)) == INVALID
+    assert "layer 1" in last_error(mq4)
+    mis = (_Layer * 2)(good, _Layer(*([A16, A16 + 8] + [A16] * 8)))
+    assert call(layers=ctypes.cast(mis, ctypes.c_void_p)) == ALIGN

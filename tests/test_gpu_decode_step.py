@@ -1,0 +1,189 @@
+"""The whole decode step in one launch (mq4_decode_step / DecodeStep).
+
+The persistent kernel evaluates, for one token,
+
+    for each layer:  x = x + down(swiglu(gate n, up n)),  n = rms_norm(x, norm_l)
+    token = argmax(lm_head(rms_norm(x, final_norm)))
+
+(src/model/marlin.cpp:141-142, 31-35, 145, 161-169; src/sampling/sampler.cpp:14-16)
+with the same per-element arithmetic, in the same order, as the separate
+entry points mq4_rmsnorm_gate_up_silu, mq4_qmm_residual and
+mq4_rmsnorm_lm_head_argmax.  Those are pinned step by step against the
+oracle in test_gpu_parity.py, so the bar here is bit-identity with chaining
+them: the same final hidden state and the same token.  One small case is also
+pinned directly against the oracle's fp64 chain (bars of the separate tests).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev_bf16, to_host_u16
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+H, I = 2048, 6144
+
+
+def build_model(mq4, n_layers, vocab, dev):
+    layers = []
+    for l in range(n_layers):
+        ws = [mq4.fill_normal_bf16((I, H) if p < 2 else (H, I), mq4.stream_id_layer(l, p), 0.0, 0.02, device=dev)
+              for p in range(3)]
+        norm = mq4.fill_normal_bf16((H,), mq4.stream_id_layer_norm(l), 0.1, 0.02, device=dev)
+        layers.append(mq4.DecoderLayer(norm, mq4.MLPWeights(*[mq4.quantize_weight(w) for w in ws])))
+        del ws
+    lm_w = mq4.fill_normal_bf16((vocab, H), mq4.STREAM_LM_HEAD, 0.0, 0.02, device=dev)
+    lm = mq4.quantize_weight(lm_w)
+    del lm_w
+    final_norm = mq4.fill_normal_bf16((H,), mq4.STREAM_NORM_WEIGHT, 0.1, 0.02, device=dev)
+    return layers, final_norm, lm
+
+
+def separate(mq4, x, layers, final_norm, lm):
+    """The same step through the separate entry points."""
+    x = x.reshape(1, H)
+    for ly in layers:
+        h = mq4.mlp_gate_up_silu(x, ly.mlp.gate_proj, ly.mlp.up_proj, ly.post_attn_norm, EPS)
+        x = mq4.qmatmul_residual(h, ly.mlp.down_proj, x)
+    idx, logits = mq4.lm_head_argmax(x, lm, return_logits=True, norm_weight=final_norm, eps=EPS)
+    return x, idx, logits
+
+
+def assert_same_bits(got, want, what):
+    got, want = to_host_u16(got).reshape(-1), to_host_u16(want).reshape(-1)
+    diff = np.nonzero(got != want)[0]
+    if diff.size:
+        d = np.abs(got[diff].astype(np.int64) - want[diff].astype(np.int64))
+        raise AssertionError(f"{what}: {diff.size} of {got.size} bf16 values differ "
+                             f"(first at {diff[:8].tolist()}, max bit-pattern distance {int(d.max())})")
+
+
+def token_row(m, dev, mq4):
+    return mq4.fill_normal_bf16((H,), mq4.stream_id_decode_row(m), 0.0, 1.0, device=dev)
+
+
+@pytest.mark.parametrize("n_layers,vocab", [(0, 4096), (1, 4096), (2, 1000), (3, 8193), (1, 1)])
+def test_decode_step_equals_separate_kernels(mq4, dev, n_layers, vocab):
+    print(f"decode step: layers={n_layers} vocab={vocab}", flush=True)
+    layers, fnorm, lm = build_model(mq4, n_layers, vocab, dev)
+    step = mq4.DecodeStep(layers, fnorm, lm, EPS)
+    x = token_row(0, dev, mq4)
+    x_out = torch.full((H,), float("nan"), dtype=torch.bfloat16, device=dev)
+    idx = step(x, x_out)
+    xs, idx_s, _ = separate(mq4, x, layers, fnorm, lm)
+    torch.cuda.synchronize()
+    assert_same_bits(x_out, xs, "hidden state")
+    assert int(idx.item()) == int(idx_s.item())
+    assert 0 <= int(idx.item()) < vocab
+
+
+def test_decode_step_full_model_24_layers(mq4, dev):
+    """The benchmark's shape: 24 layers, vocab 248320, three tokens in a row on
+    one workspace (the phase tags advance per call)."""
+    print("decode step: layers=24 vocab=248320", flush=True)
+    layers, fnorm, lm = build_model(mq4, 24, 248320, dev)
+    step = mq4.DecodeStep(layers, fnorm, lm, EPS)
+    x_out = torch.empty((H,), dtype=torch.bfloat16, device=dev)
+    for m in range(3):
+        x = token_row(m, dev, mq4)
+        idx = step(x, x_out)
+        xs, idx_s, logits = separate(mq4, x, layers, fnorm, lm)
+        torch.cuda.synchronize()
+        assert_same_bits(x_out, xs, f"hidden state, token {m}")
+        assert int(idx.item()) == int(idx_s.item()), f"token {m}"
+        lg = logits.float().reshape(-1)
+        assert float(lg[int(idx.item())]) == float(lg.max())
+    ctrl = step.workspace[:4].view(torch.int32)
+    assert int(ctrl.item()) == 3        # one completed call per token
+
+
+def test_decode_step_against_oracle(mq4, O, dev):
+    """One layer, vocab 4096, against the oracle's fp64 chain: the hidden state
+    within rms(err) <= 1e-2 rms, and the token's fp64 logit within 1e-2 rms of
+    the fp64 maximum (an exact argmax of two correct implementations can only
+    differ on a near-tie)."""
+    layers, fnorm, lm = build_model(mq4, 1, 4096, dev)
+    step = mq4.DecodeStep(layers, fnorm, lm, EPS)
+    x = token_row(0, dev, mq4)
+    x_out = torch.empty((H,), dtype=torch.bfloat16, device=dev)
+    tok = int(step(x, x_out).item())
+    torch.cuda.synchronize()
+
+    def q(w):
+        return (w.weight.cpu().numpy().view(np.uint32), to_host_u16(w.scales), to_host_u16(w.biases))
+
+    xh = to_host_u16(x).reshape(1, H)
+    ly = layers[0]
+    n = O.rmsnorm_1pw(xh, to_host_u16(ly.post_attn_norm), EPS)
+    _, _, _, yb = O.mlp_forward(n, q(ly.mlp.gate_proj), q(ly.mlp.up_proj), q(ly.mlp.down_proj))
+    ref = O.add_bf16(xh, yb)
+    rf = O.bf16_to_f32(ref).astype(np.float64).reshape(-1)
+    got = O.bf16_to_f32(to_host_u16(x_out)).astype(np.float64)
+    rms = float(np.sqrt(np.mean(rf * rf)))
+    assert float(np.sqrt(np.mean((got - rf) ** 2))) <= 1e-2 * rms
+    hn = O.rmsnorm_1pw(ref, to_host_u16(fnorm), EPS)
+    l64, _ = O.qmm_f64(hn, *q(lm))
+    l64 = l64.reshape(-1)
+    lrms = float(np.sqrt(np.mean(l64 * l64)))
+    assert l64.max() - l64[tok] <= 1e-2 * lrms
+
+
+def test_decode_step_graph_replay(mq4, dev):
+    """Captured once in a HIP graph and replayed with eager work in between:
+    every replay gives the eager result."""
+    layers, fnorm, lm = build_model(mq4, 2, 4096, dev)
+    step = mq4.DecodeStep(layers, fnorm, lm, EPS)
+    x = token_row(1, dev, mq4)
+    x_out = torch.empty((H,), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((1,), dtype=torch.int32, device=dev)
+    step(x, x_out, idx)
+    torch.cuda.synchronize()
+    want_x, want_i = to_host_u16(x_out).copy(), int(idx.item())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(x, x_out, idx)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(x, x_out, idx)
+    for r in range(3):
+        x_out.fill_(0)
+        idx.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host_u16(x_out), want_x), f"replay {r}"
+        assert int(idx.item()) == want_i, f"replay {r}"
+        separate(mq4, x, layers, fnorm, lm)        # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_decode_step_sticky_error(mq4, dev):
+    """A workspace whose error word is set makes every call return token
+    0xFFFFFFFF without touching x_out, until the workspace is zero-filled."""
+    layers, fnorm, lm = build_model(mq4, 1, 4096, dev)
+    step = mq4.DecodeStep(layers, fnorm, lm, EPS)
+    x = token_row(2, dev, mq4)
+    x_out = torch.zeros((H,), dtype=torch.bfloat16, device=dev)
+    step.workspace[128:132].view(torch.int32).fill_(1)       # error word (uint32 index 32)
+    idx = step(x, x_out)
+    torch.cuda.synchronize()
+    assert int(idx.item()) == -1
+    assert not bool(x_out.view(torch.int16).any())
+    step.reset()
+    idx = step(x, x_out)
+    _, idx_s, _ = separate(mq4, x, layers, fnorm, lm)
+    torch.cuda.synchronize()
+    assert int(idx.item()) == int(idx_s.item())
+
+
+def test_decode_step_rejects_other_shapes(mq4, dev):
+    w = mq4.quantize_weight(mq4.fill_normal_bf16((256, 1024), 5, 0.0, 0.02, device=dev))
+    fn = torch.zeros((1024,), dtype=torch.bfloat16, device=dev)
+    step = mq4.DecodeStep([], fn, w, EPS)
+    with pytest.raises(mq4.MQ4Error) as e:
+        step(torch.zeros((1024,), dtype=torch.bfloat16, device=dev))
+    assert e.value.code == -2
