@@ -155,8 +155,9 @@ __device__ __forceinline__ float slice_d(const uint4& w, const uint32_t* xp) {
 // Normalize xraw (H bf16) with (1 + w) RMSNorm and build xp/xs.  Every I/O
 // wave computes the full sum of squares (lane l sums the 16 words of slice l,
 // then the wave reduces: the order of the separate kernels) and handles a
-// quarter of the slices, 4 lanes per slice, one 16-byte chunk per lane.
-__device__ void stage_norm_x(Smem& sm, const uint16_t* norm_w, float eps, int io, int lane) {
+// quarter of the slices, 4 lanes per slice, one 16-byte chunk per lane; nw is
+// this lane's chunk of the norm weight, loaded a layer ahead.
+__device__ void stage_norm_x(Smem& sm, const uint4 nw, float eps, int io, int lane) {
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -166,20 +167,18 @@ __device__ void stage_norm_x(Smem& sm, const uint16_t* norm_w, float eps, int io
         ss = sumsq_word(ss, v.z);
         ss = sumsq_word(ss, v.w);
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    ss = wave_sum(ss);
     const float r = rms_inv(ss, H, eps);
     constexpr int SPW = SA / kNIO;                 // 16 slices per I/O wave
     const int sl = io * SPW + (lane >> 2);
     const int q = lane & 3;
-    const uint4 nw = reinterpret_cast<const uint4*>(norm_w)[sl * 4 + q];
     const uint4 xv = reinterpret_cast<const uint4*>(sm.xraw)[sl * 4 + q];
     const uint4 xn = make_uint4(norm_word(xv.x, nw.x, r), norm_word(xv.y, nw.y, r), norm_word(xv.z, nw.z, r),
                                 norm_word(xv.w, nw.w, r));
     uint32_t pr[4];
     const float c = pair_chunk(xn, pr, 0.0f);
     *reinterpret_cast<uint4*>(&sm.xp[sl][4 * q]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-    const float c1 = __shfl_down(c, 1), c2 = __shfl_down(c, 2), c3 = __shfl_down(c, 3);
+    const float c1 = quad_lane<1>(c), c2 = quad_lane<2>(c), c3 = quad_lane<3>(c);
     if (q == 0) sm.xs[sl] = ((c + c1) + c2) + c3;
 }
 
@@ -212,6 +211,11 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     if (wave < kNIO) {
         // ============================ I/O waves ============================
         const int io = wave;
+        // this lane's 16-byte chunk of a norm weight (slice io*16 + lane/4,
+        // chunk lane%4), loaded one layer ahead of its use
+        const int nchunk = (io * (SA / kNIO) + (lane >> 2)) * 4 + (lane & 3);
+        auto norm_of = [&](int l) { return l < L ? p.layers[l].norm : p.final_norm; };
+        uint4 nw = reinterpret_cast<const uint4*>(norm_of(0))[nchunk];
         for (int l = 0; l <= L; ++l) {
             // ---- x of layer l (the input at l == 0) -> xraw ----
             if (l == 0) {
@@ -228,9 +232,10 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
             }
             __syncthreads();                                   // B1: xraw complete
             if (sm.abort) break;
-            stage_norm_x(sm, l < L ? p.layers[l].norm : p.final_norm, p.eps, io, lane);
+            stage_norm_x(sm, nw, p.eps, io, lane);
             __syncthreads();                                   // B2: xp/xs ready
             if (l == L) break;
+            nw = reinterpret_cast<const uint4*>(norm_of(l + 1))[nchunk];
             __syncthreads();                                   // B3: h slice in sm.out
             if (io == 0 && lane < I / kNWG / 2)
                 st_tagged(p.hbuf + wg * (I / kNWG / 2) + lane,
@@ -374,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
                 for (int t = 0; t < 2; ++t)
                     acc[r * 2 + t] += affine_term(sa[t][r], ba[t][r], slice_d(wa[t][r], xp), xs);
             const float v = wave_multi_reduce<8>(acc, lane);
-            const float other = __shfl_xor(v, 8);        // up partner of gate value index v^1
+            const float other = dpp_partner_f(v, 8);     // up partner (value index v^1, lane l^8)
             const int vidx = lane >> 3;
             if ((lane & 7) == 0 && (vidx & 1) == 0 && (vidx >> 1) < RA)
                 sm.out[cw * RA + (vidx >> 1)] = swiglu_bf16(v, other);
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
                 acc[j] += affine_term(sb[0][j], bb[0][j], slice_d(wb[0][j], hp), sm.hs[sl]);
             }
             const float v = wave_multi_reduce<4>(acc, lane);    // lane >> 4 = third
-            const float v0 = __shfl(v, 0), v1 = __shfl(v, 16), v2 = __shfl(v, 32);
+            const float v0 = lane_value(v, 0), v1 = lane_value(v, 16), v2 = lane_value(v, 32);
             float y = 0.0f;
             y += v0;
             y += v1;

@@ -49,9 +49,20 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 
 // Nibbles p and p+4 of a packed word as the bf16 pair (128 + q_p, 128 + q_{p+4}):
 // 0x4300 is bf16 128.0 and its 7 mantissa bits hold q exactly.
+// One v_and_or_b32 per pair (plus a shift for P > 0): the compiler emits a
+// separate AND and OR because gfx9 VOP3 encodings take no literal constant,
+// so the mask is passed in an SGPR and the exponent bits in a VGPR.
 template <int P>
 __device__ __forceinline__ uint32_t nib_pair_bf16(uint32_t word) {
-    return ((word >> (4 * P)) & 0x000F000Fu) | 0x43004300u;
+    const uint32_t s = P ? (word >> (4 * P)) : word;
+#ifdef NO_ANDOR
+    return (s & 0x000F000Fu) | 0x43004300u;
+#else
+    uint32_t m, c;
+    asm("s_mov_b32 %0, 0x000f000f" : "=s"(m));
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(c));
+    return (s & m) | c;
+#endif
 }
 
 // ---- per-element arithmetic shared by every decode kernel ----
@@ -136,32 +147,117 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
     return 0xffffffffu - (uint32_t)(key & 0xffffffffu);
 }
 
+// ---- cross-lane butterfly on the VALU (no LDS round trip) ----
+// Level OFF pairs lane l with partner(l): OFF = 32 -> l^32 and 16 -> l^16
+// (v_permlane32_swap / v_permlane16_swap, which move two registers at once),
+// 8 -> l^8 (DPP row_ror:8 within a 16-lane row), 4 -> l^7 (DPP
+// row_half_mirror), 2 -> l^2 and 1 -> l^1 (DPP quad_perm).  Each level flips
+// bit log2(OFF) of the lane index, and the six partners span all 64 lanes, so
+// six levels sum every lane exactly once.
+template <int OFF>
+__device__ __forceinline__ uint32_t dpp_partner(uint32_t v) {
+    static_assert(OFF == 8 || OFF == 4 || OFF == 2 || OFF == 1, "DPP levels");
+    constexpr int ctrl = OFF == 8 ? 0x128 : OFF == 4 ? 0x141 : OFF == 2 ? 0x4E : 0xB1;
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float dpp_partner_f(float v, int off) {
+    switch (off) {
+        case 8: return __uint_as_float(dpp_partner<8>(__float_as_uint(v)));
+        case 4: return __uint_as_float(dpp_partner<4>(__float_as_uint(v)));
+        case 2: return __uint_as_float(dpp_partner<2>(__float_as_uint(v)));
+        default: return __uint_as_float(dpp_partner<1>(__float_as_uint(v)));
+    }
+}
+
+// Value of v in lane `src` (wave-uniform result).  The readlane builtin is
+// typed int, so the float travels as its bit pattern.
+__device__ __forceinline__ float lane_value(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// Value of lane K of this lane's quad (DPP quad_perm broadcast).
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+    constexpr int ctrl = K | (K << 2) | (K << 4) | (K << 6);
+    return __uint_as_float((uint32_t)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), ctrl, 0xF, 0xF, false));
+}
+
+// (a', b') of v_permlane32_swap / v_permlane16_swap on (a, b): in the lower
+// half of each pair of lane groups a' = a and b' = a of the partner lane; in
+// the upper half a' = b of the partner lane and b' = b.  So a' + b' is the
+// pair sum of a in the lower half and of b in the upper half.
+template <int OFF>
+__device__ __forceinline__ void swap_halves(float a, float b, float& a2, float& b2) {
+    static_assert(OFF == 32 || OFF == 16, "swap levels");
+    if constexpr (OFF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        a2 = __uint_as_float(r[0]);
+        b2 = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        a2 = __uint_as_float(r[0]);
+        b2 = __uint_as_float(r[1]);
+    }
+}
+
+// Sum of v over the 64 lanes (every lane receives it).
+__device__ __forceinline__ float wave_sum(float v) {
+    float a, b;
+    swap_halves<32>(v, v, a, b);
+    v = a + b;
+    swap_halves<16>(v, v, a, b);
+    v = a + b;
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) v += dpp_partner_f(v, off);
+    return v;
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    uint32_t lo = __shfl_xor((uint32_t)v, m);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+    const uint32_t lo = __shfl_xor((uint32_t)v, m);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
     return ((uint64_t)hi << 32) | lo;
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
-        uint64_t o = shfl_xor_u64(v, m);
+        const uint64_t o = shfl_xor_u64(v, m);
         v = o > v ? o : v;
     }
     return v;
 }
 
 // Reduce V per-lane values (V a power of two, 1..64) over the 64 lanes of a
-// wave by recursive halving: at each xor step a lane keeps one half of its
-// values and adds the partner's copy of that half.  Afterwards v[0] of lane l
-// holds the wave-wide sum of value index (l >> (6 - log2 V)); the lanes with
-// (l & (64/V - 1)) == 0 are the designated holders of each index.
+// wave by recursive halving over the butterfly levels 32, 16, 8, 4, 2, 1: at
+// each level the lanes of the lower half (bit log2(level) clear) keep the
+// first half of their values and the upper lanes the second half, each adding
+// the partner's copy.  Afterwards v[0] of lane l holds the wave-wide sum of
+// value index (l >> (6 - log2 V)), identical in all lanes of that index.
 template <int V>
 __device__ __forceinline__ float wave_multi_reduce(float (&v)[V], int lane) {
     static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
     int count = V;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
+    for (int lvl = 0; lvl < 2; ++lvl) {          // levels 32 and 16
+        const int h = count > 1 ? count >> 1 : 0;
+#pragma unroll
+        for (int i = 0; i < (V > 1 ? V / 2 : 1); ++i) {
+            if (count == 1 && i == 0) {
+                float a, b;
+                if (lvl == 0) swap_halves<32>(v[0], v[0], a, b);
+                else swap_halves<16>(v[0], v[0], a, b);
+                v[0] = a + b;
+            } else if (i < h) {
+                float a, b;
+                if (lvl == 0) swap_halves<32>(v[i], v[i + h], a, b);
+                else swap_halves<16>(v[i], v[i + h], a, b);
+                v[i] = a + b;
+            }
+        }
+        if (count > 1) count = h;
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
         if (count > 1) {
             const bool upper = (lane & off) != 0;
             const int h = count >> 1;
@@ -173,12 +269,12 @@ __device__ __forceinline__ float wave_multi_reduce(float (&v)[V], int lane) {
                     const float lo = v[i], hi = v[i + h];
                     const float send = upper ? lo : hi;
                     const float keep = upper ? hi : lo;
-                    v[i] = keep + __shfl_xor(send, off);
+                    v[i] = keep + dpp_partner_f(send, off);
                 }
             }
             count = h;
         } else {
-            v[0] += __shfl_xor(v[0], off);
+            v[0] += dpp_partner_f(v[0], off);
         }
     }
     return v[0];

@@ -151,9 +151,7 @@ __global__ __launch_bounds__(64 * KS * NG) void q4_gemv_kernel(GemvParams p) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) s = sumsq_word(s, e[q]);
                 }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-            ss[m] = s;
+            ss[m] = wave_sum(s);
         }
         if (KS > 1) {
             if (lane == 0)
@@ -395,8 +393,7 @@ __global__ __launch_bounds__(256) void rms_norm_1pw_kernel(const uint16_t* __res
         const float v = bf16_to_f32(xr[k]);
         ss += v * v;
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    ss = wave_sum(ss);
     __shared__ float part[4];
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
     __syncthreads();
