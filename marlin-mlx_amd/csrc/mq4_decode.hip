@@ -46,6 +46,8 @@ constexpr int kNIO = 4;              // I/O waves per workgroup
 constexpr int kNCW = 8;              // compute waves per workgroup
 constexpr int kThreads = 64 * (kNIO + kNCW);
 constexpr int kMaxLayers = 32;
+constexpr int kCopies = 8;           // replicas of the exchange buffers (one per XCD)
+constexpr int kFirstPollSleep = 20;  // s_sleep units (64 clocks) before the first poll round
 constexpr int H = 2048;              // hidden size this instance is built for
 constexpr int I = 6144;              // intermediate size
 constexpr int SA = H / 32;           // 16-byte slices per gate/up row (64)
@@ -54,7 +56,7 @@ constexpr int SPL_B = SB / 64;       // down slices per lane (3)
 constexpr int RA = I / kNWG / kNCW;  // gate/up rows per compute wave (3)
 constexpr int RB = H / kNWG / kNCW;  // down rows per compute wave (1)
 constexpr int LM_RPI = 4;            // lm_head rows per batch
-constexpr int LM_NBUF = 3;           // lm_head batches in flight per compute wave
+constexpr int LM_NBUF = 2;           // lm_head batches in flight per compute wave
 static_assert(SA == 64 && SB % 64 == 0 && RA * kNWG * kNCW == I && RB * kNWG * kNCW == H, "shape");
 
 struct Layer {
@@ -71,8 +73,8 @@ struct Params {
     QMat lm;
     int vocab;
     int n_layers;
-    uint64_t* xbuf;            // [H/2] tagged words
-    uint64_t* hbuf;            // [I/2] tagged words
+    uint64_t* xbuf;            // [kCopies][H/2] tagged words
+    uint64_t* hbuf;            // [kCopies][I/2] tagged words
     uint64_t* part;            // [kNWG] tagged per-workgroup argmax keys
     uint32_t* ctrl;            // [0] epoch, [32] sticky error flag
     int spin_limit;
@@ -98,6 +100,11 @@ template <int NW>
 __device__ bool poll_words(const uint64_t* src, uint32_t tag, uint32_t* dst, const Params& p, int lane) {
     constexpr int PER = NW / 64;
     uint64_t w[PER];
+    // The first round is delayed by ~0.5 us: issued right after this
+    // workgroup's own publish it meets the other workgroups' stores still in
+    // flight and takes ~1.5 us to return (and fails), while a round issued
+    // slightly later returns in ~0.6 us with the phase complete.
+    __builtin_amdgcn_s_sleep(kFirstPollSleep);
     for (int spins = 0;; ++spins) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) w[i] = ld_tagged(src + i * 64 + lane);
@@ -125,6 +132,37 @@ __device__ __forceinline__ void pair_slice(const uint32_t* words, uint32_t* out1
     *sum = s;
 }
 
+// Per-compute-wave LDS staging of one layer's weights (filled by LDS DMA):
+// gate/up rows rowA..rowA+RA-1 of both matrices, and the down row.
+struct alignas(16) WStageA {
+    uint4 w[2][RA][64];            // 16-byte slices, lane-major
+    uint32_t s[2][64];             // the RA*32 bf16 scales of each matrix (dwords 0..47)
+    uint32_t b[2][64];             // biases, same layout
+};
+struct alignas(16) WStageB {
+    uint4 w[SPL_B][64];
+    uint32_t s[64];                // the 96 bf16 scales of the down row (dwords 0..47)
+    uint32_t b[64];
+};
+constexpr int kDmaA = 2 * (RA + 2);  // LDS DMA instructions per gate/up stage
+constexpr int kDmaB = SPL_B + 2;     // per down stage
+
+// Workgroup barrier without a memory fence: waits for this wave's LDS
+// operations only (lgkmcnt), not for outstanding global loads or LDS DMA.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Pin a value in a VGPR at this point of the program: the computation that
+// produces it cannot be moved below (e.g. below a barrier) by the compiler.
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 struct alignas(16) Smem {
     uint32_t xraw[H / 2];          // raw x of the current layer (residual), bf16 pairs
     uint32_t xp[SA][16];           // dot2-paired normalized x per slice
@@ -149,6 +187,14 @@ __device__ __forceinline__ float slice_d(const uint4& w, const uint32_t* xp) {
         d = dot2_bf16(xp[4 * k + 2], nib_pair_bf16<2>(wd[k]), d);
         d = dot2_bf16(xp[4 * k + 3], nib_pair_bf16<3>(wd[k]), d);
     }
+    return d;
+}
+
+// The same dot2 chain over pre-unpacked nibble pairs (nib_pairs of the four words).
+__device__ __forceinline__ float pairs_d(const uint32_t* pr, const uint32_t* xp) {
+    float d = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d = dot2_bf16(xp[i], pr[i], d);
     return d;
 }
 
@@ -193,6 +239,8 @@ __device__ void stage_h(Smem& sm, int io, int lane) {
 
 __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     __shared__ Smem sm;
+    __shared__ WStageA wsa[kNCW];
+    __shared__ WStageB wsb[kNCW];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wg = blockIdx.x;
     const int L = p.n_layers;
@@ -208,14 +256,74 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         return;
     }
 
+    // LDS DMA of one layer's weights into compute wave c's staging buffers
+    // (issued by the I/O waves, see below).
+    const int sdw = lane < 48 ? lane : 47;           // dword of a 192-byte scale/bias run
+    auto dmaA = [&](int c, int l, int t) {           // kDmaA / 2 instructions (t: 0 gate, 1 up)
+        const Layer& Ly = p.layers[l];
+        const int rowA = wg * (I / kNWG) + c * RA;
+        {
+            const QMat& Q = t == 0 ? Ly.gate : Ly.up;
+#pragma unroll
+            for (int r = 0; r < RA; ++r)
+                __builtin_amdgcn_global_load_lds(
+                    reinterpret_cast<const uint4*>(Q.wq + (int64_t)(rowA + r) * (H / 8)) + lane, &wsa[c].w[t][r][0], 16, 0,
+                    0);
+            // scales/biases of the RA consecutive rows: RA*32 bf16 = 192 bytes
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(Q.s + (int64_t)rowA * (H / 64)) + sdw,
+                                             &wsa[c].s[t][0], 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(Q.b + (int64_t)rowA * (H / 64)) + sdw,
+                                             &wsa[c].b[t][0], 4, 0, 0);
+        }
+    };
+    auto dmaB = [&](int c, int l) {                  // kDmaB instructions
+        const QMat& Q = p.layers[l].down;
+        const int rowB = wg * (H / kNWG) + c * RB;
+#pragma unroll
+        for (int j = 0; j < SPL_B; ++j)
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const uint4*>(Q.wq + (int64_t)rowB * (I / 8)) + j * 64 + lane, &wsb[c].w[j][0], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(Q.s + (int64_t)rowB * (I / 64)) + sdw,
+                                         &wsb[c].s[0], 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(Q.b + (int64_t)rowB * (I / 64)) + sdw,
+                                         &wsb[c].b[0], 4, 0, 0);
+    };
+    static_assert(kNCW == 2 * kNIO, "each I/O wave stages the weights of two compute waves");
+    static_assert(kDmaA % 2 == 0, "gate and up halves");
+
     if (wave < kNIO) {
         // ============================ I/O waves ============================
+        // Weights reach the compute waves' LDS staging buffers by DMA, issued
+        // only in phases without a poll in flight (weight traffic ahead of a
+        // poll in the CU's memory pipeline delays it) and by waves idle in
+        // that phase, since issuing stalls the issuing wave for about the
+        // transfer time (~0.9 us for 28 KB per CU at its HBM share):
+        //   gate rows of layer l+1: each compute wave, RMSNorm phase of l;
+        //   up rows of layer l+1:   I/O waves, gate/up phase of l, waited by B5;
+        //   down row of layer l+1:  I/O waves, down phase of l, waited by B3 of l+1.
+        // I/O wave io serves compute waves 2*io and 2*io+1.  The barriers
+        // carry no memory fence (lds_barrier): a fence would wait for all
+        // outstanding DMA.
         const int io = wave;
         // this lane's 16-byte chunk of a norm weight (slice io*16 + lane/4,
         // chunk lane%4), loaded one layer ahead of its use
         const int nchunk = (io * (SA / kNIO) + (lane >> 2)) * 4 + (lane & 3);
         auto norm_of = [&](int l) { return l < L ? p.layers[l].norm : p.final_norm; };
         uint4 nw = reinterpret_cast<const uint4*>(norm_of(0))[nchunk];
+        // the copy of the exchange buffers this workgroup reads
+        const uint64_t* xcopy = p.xbuf + (size_t)(wg % kCopies) * (H / 2);
+        const uint64_t* hcopy = p.hbuf + (size_t)(wg % kCopies) * (I / 2);
+        constexpr int kIoA = kDmaA, kIoB = 2 * kDmaB;   // up halves of two waves; two down rows
+        if (L > 0) {
+            dmaA(2 * io, 0, 0);
+            dmaA(2 * io, 0, 1);
+            dmaA(2 * io + 1, 0, 0);
+            dmaA(2 * io + 1, 0, 1);
+            dmaB(2 * io, 0);
+            dmaB(2 * io + 1, 0);
+            wait_vmcnt<kIoB>();
+        }
+        lds_barrier();                                         // B0: gate/up weights of layer 0 staged
         for (int l = 0; l <= L; ++l) {
             // ---- x of layer l (the input at l == 0) -> xraw ----
             if (l == 0) {
@@ -226,21 +334,34 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
                     sm.xraw[word] = v;
                     if (L == 0 && wg == 0 && p.x_out) reinterpret_cast<uint32_t*>(p.x_out)[word] = v;
                 }
-            } else if (!poll_words<H / 2 / kNIO>(p.xbuf + io * (H / 2 / kNIO), base + 2 * l,
+            } else if (!poll_words<H / 2 / kNIO>(xcopy + io * (H / 2 / kNIO), base + 2 * l,
                                                  sm.xraw + io * (H / 2 / kNIO), p, lane)) {
                 sm.abort = 1;
             }
-            __syncthreads();                                   // B1: xraw complete
+            lds_barrier();                                     // B1: xraw complete
             if (sm.abort) break;
             stage_norm_x(sm, nw, p.eps, io, lane);
-            __syncthreads();                                   // B2: xp/xs ready
+            lds_barrier();                                     // B2: xp/xs ready
             if (l == L) break;
             nw = reinterpret_cast<const uint4*>(norm_of(l + 1))[nchunk];
-            __syncthreads();                                   // B3: h slice in sm.out
-            if (io == 0 && lane < I / kNWG / 2)
-                st_tagged(p.hbuf + wg * (I / kNWG / 2) + lane,
-                          ((uint64_t)(base + 2 * l + 1) << 32) | (sm.out[2 * lane] | (sm.out[2 * lane + 1] << 16)));
-            if (!poll_words<I / 2 / kNIO>(p.hbuf + io * (I / 2 / kNIO), base + 2 * l + 1,
+            if (l + 1 < L) {
+                dmaA(2 * io, l + 1, 1);
+                dmaA(2 * io + 1, l + 1, 1);
+                wait_vmcnt<kIoA>();                            // down weights of layer l staged
+            } else {
+                wait_vmcnt<0>();
+            }
+            lds_barrier();                                     // B3: h slice in sm.out
+            {   // this workgroup's h words into every copy
+                constexpr int HW = I / kNWG / 2;
+                const int i = io * 64 + lane;
+                if (i < HW * kCopies) {
+                    const int c = i / HW, w = i - c * HW;
+                    st_tagged(p.hbuf + (size_t)c * (I / 2) + wg * HW + w,
+                              ((uint64_t)(base + 2 * l + 1) << 32) | (sm.out[2 * w] | (sm.out[2 * w + 1] << 16)));
+                }
+            }
+            if (!poll_words<I / 2 / kNIO>(hcopy + io * (I / 2 / kNIO), base + 2 * l + 1,
                                           sm.hraw + io * (I / 2 / kNIO), p, lane))
                 sm.abort = 1;
             // the words this wave polled are exactly the slices it pairs
@@ -248,16 +369,26 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             stage_h(sm, io, lane);
-            __syncthreads();                                   // B4: hp/hs ready
+            lds_barrier();                                     // B4: hp/hs ready
             if (sm.abort) break;
-            __syncthreads();                                   // B5: new x rows in sm.out
-            if (io == 0 && lane < H / kNWG / 2) {
-                const uint32_t v = sm.out[2 * lane] | (sm.out[2 * lane + 1] << 16);
-                st_tagged(p.xbuf + wg * (H / kNWG / 2) + lane, ((uint64_t)(base + 2 * l + 2) << 32) | v);
-                if (l == L - 1 && p.x_out)
-                    reinterpret_cast<uint32_t*>(p.x_out)[wg * (H / kNWG / 2) + lane] = v;
+            if (l + 1 < L) {
+                dmaB(2 * io, l + 1);
+                dmaB(2 * io + 1, l + 1);
+                wait_vmcnt<kIoB>();                            // up weights of layer l+1 staged
+            }
+            lds_barrier();                                     // B5: new x rows in sm.out
+            {   // this workgroup's new x words into every copy
+                constexpr int XW = H / kNWG / 2;
+                const int i = io * 64 + lane;
+                if (i < XW * kCopies) {
+                    const int c = i / XW, w = i - c * XW;
+                    const uint32_t v = sm.out[2 * w] | (sm.out[2 * w + 1] << 16);
+                    st_tagged(p.xbuf + (size_t)c * (H / 2) + wg * XW + w, ((uint64_t)(base + 2 * l + 2) << 32) | v);
+                    if (c == 0 && l == L - 1 && p.x_out) reinterpret_cast<uint32_t*>(p.x_out)[wg * XW + w] = v;
+                }
             }
         }
+        wait_vmcnt<0>();                                       // no DMA may outlive the workgroup
         // ---- argmax: this workgroup's best key, then workgroup 0 reduces ----
         __syncthreads();                                       // B6: sm.best filled
         const uint32_t tag16 = (sm.epoch % 65535u) + 1u;
@@ -298,39 +429,65 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
 
     // ============================ compute waves ============================
     const int cw = wave - kNIO;
-    // weights of the next gate/up and down phases, loaded one phase ahead
-    uint4 wa[2][RA];
-    uint32_t sa[2][RA], ba[2][RA];
-    uint4 wb[RB][SPL_B];
-    uint32_t sb[RB][SPL_B], bb[RB][SPL_B];
-    const int rowA = wg * (I / kNWG) + cw * RA;     // first gate/up row of this wave
+    // This wave's weights arrive in its LDS staging buffers by DMA (issued
+    // and awaited by the I/O waves, no registers held while in flight) and
+    // are unpacked into bf16 nibble pairs while the activations are being
+    // exchanged: gate/up weights of layer l after B5 of layer l-1, down
+    // weights after B3.  The compute waves issue no memory operation inside
+    // the layer loop, so their barriers carry no fence (lds_barrier).
+    WStageA& SA_ = wsa[cw];
+    WStageB& SB_ = wsb[cw];
     const int rowB = wg * (H / kNWG) + cw * RB;     // down row of this wave
+    static_assert(RB == 1 && SPL_B == 3, "down layout");
 
-    auto loadA = [&](int l) {
-        const Layer& Ly = p.layers[l];
+    uint32_t pa[2][RA][16];
+    float ks_a[2][RA], kc_a[2][RA];
+    auto unpackA = [&]() {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const QMat& Q = t == 0 ? Ly.gate : Ly.up;
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < RA; ++r) {
-                const int row = rowA + r;
-                wa[t][r] = load_nt_u4(reinterpret_cast<const uint4*>(Q.wq + (int64_t)row * (H / 8)) + lane);
-                sa[t][r] = Q.s[row * (H / 64) + (lane >> 1)];
-                ba[t][r] = Q.b[row * (H / 64) + (lane >> 1)];
+                const uint4 w = SA_.w[t][r][lane];
+                nib_pairs(w.x, &pa[t][r][0]);
+                nib_pairs(w.y, &pa[t][r][4]);
+                nib_pairs(w.z, &pa[t][r][8]);
+                nib_pairs(w.w, &pa[t][r][12]);
+                const int g = r * (H / 64) + (lane >> 1);
+                ks_a[t][r] = bf16_to_f32(reinterpret_cast<const uint16_t*>(SA_.s[t])[g]);
+                kc_a[t][r] = affine_c(ks_a[t][r], reinterpret_cast<const uint16_t*>(SA_.b[t])[g]);
             }
-        }
+        // done now, while the exchange runs, not after the next barrier
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < RA; ++r) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) pin(pa[t][r][i]);
+                pin(ks_a[t][r]);
+                pin(kc_a[t][r]);
+            }
     };
-    auto loadB = [&](int l) {
-        const QMat& Q = p.layers[l].down;
+    uint32_t pb[SPL_B][16];
+    float ks_b[SPL_B], kc_b[SPL_B];
+    auto unpackB = [&]() {
 #pragma unroll
-        for (int r = 0; r < RB; ++r)
+        for (int j = 0; j < SPL_B; ++j) {
+            const uint4 w = SB_.w[j][lane];
+            nib_pairs(w.x, &pb[j][0]);
+            nib_pairs(w.y, &pb[j][4]);
+            nib_pairs(w.z, &pb[j][8]);
+            nib_pairs(w.w, &pb[j][12]);
+            const int g = (j * 64 + lane) >> 1;
+            ks_b[j] = bf16_to_f32(reinterpret_cast<const uint16_t*>(SB_.s)[g]);
+            kc_b[j] = affine_c(ks_b[j], reinterpret_cast<const uint16_t*>(SB_.b)[g]);
+        }
 #pragma unroll
-            for (int j = 0; j < SPL_B; ++j) {
-                const int row = rowB + r, sl = j * 64 + lane;
-                wb[r][j] = load_nt_u4(reinterpret_cast<const uint4*>(Q.wq + (int64_t)row * (I / 8)) + sl);
-                sb[r][j] = Q.s[row * (I / 64) + (sl >> 1)];
-                bb[r][j] = Q.b[row * (I / 64) + (sl >> 1)];
-            }
+        for (int j = 0; j < SPL_B; ++j) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) pin(pb[j][i]);
+            pin(ks_b[j]);
+            pin(kc_b[j]);
+        }
     };
 
     // lm_head streaming state: this wave's batches of LM_RPI rows, LM_NBUF
@@ -355,15 +512,16 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         }
     };
 
-    if (L > 0) {
-        loadA(0);
-        loadB(0);
-    }
-    bool aborted = false;
-    for (int l = 0; l < L; ++l) {
-        __syncthreads();                                       // B1
-        if (sm.abort) { aborted = true; break; }
-        __syncthreads();                                       // B2
+    // One layer; false if the step was aborted.  On entry this layer's up
+    // weights are staged and its gate weights (this wave's own DMA) issued;
+    // its down weights are staged by B3.
+    auto layer = [&](int l) -> bool {
+        wait_vmcnt<0>();                                       // own gate-row DMA
+        unpackA();                                             // while x is gathered
+        lds_barrier();                                         // B1
+        if (sm.abort) return false;
+        if (l + 1 < L) dmaA(cw, l + 1, 0);                     // during the RMSNorm phase
+        lds_barrier();                                         // B2
         // ---- gate/up rows rowA..rowA+RA-1 ----
         {
             uint32_t xp[16];
@@ -377,22 +535,21 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
             for (int r = 0; r < RA; ++r)
 #pragma unroll
                 for (int t = 0; t < 2; ++t)
-                    acc[r * 2 + t] += affine_term(sa[t][r], ba[t][r], slice_d(wa[t][r], xp), xs);
+                    acc[r * 2 + t] += affine_term_f(ks_a[t][r], kc_a[t][r], pairs_d(pa[t][r], xp), xs);
             const float v = wave_multi_reduce<8>(acc, lane);
             const float other = dpp_partner_f(v, 8);     // up partner (value index v^1, lane l^8)
             const int vidx = lane >> 3;
             if ((lane & 7) == 0 && (vidx & 1) == 0 && (vidx >> 1) < RA)
                 sm.out[cw * RA + (vidx >> 1)] = swiglu_bf16(v, other);
         }
-        if (l + 1 < L) loadA(l + 1);
-        __syncthreads();                                       // B3
-        __syncthreads();                                       // B4
-        if (sm.abort) { aborted = true; break; }
+        lds_barrier();                                         // B3
+        unpackB();                                             // while h is gathered
+        lds_barrier();                                         // B4
+        if (sm.abort) return false;
         // ---- down row rowB (+ residual) ----
         {
             // one partial per 64-slice third of K, reduced over the wave, then
             // added in order (the K-split order of the separate kernel)
-            static_assert(RB == 1 && SPL_B == 3, "down layout");
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < SPL_B; ++j) {
@@ -400,7 +557,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
                 uint32_t hp[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) hp[i] = sm.hp[sl][i];
-                acc[j] += affine_term(sb[0][j], bb[0][j], slice_d(wb[0][j], hp), sm.hs[sl]);
+                acc[j] += affine_term_f(ks_b[j], kc_b[j], pairs_d(pb[j], hp), sm.hs[sl]);
             }
             const float v = wave_multi_reduce<4>(acc, lane);    // lane >> 4 = third
             const float v0 = lane_value(v, 0), v1 = lane_value(v, 16), v2 = lane_value(v, 32);
@@ -415,9 +572,14 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
                 sm.out[cw] = f32_to_bf16(res + round_bf16(y));
             }
         }
-        if (l + 1 < L) loadB(l + 1);
-        __syncthreads();                                       // B5
-    }
+        lds_barrier();                                         // B5
+        return true;
+    };
+
+    lds_barrier();                                             // B0
+    bool aborted = false;
+    for (int l = 0; l < L; ++l)
+        if (!layer(l)) { aborted = true; break; }
 
     // ---- lm_head + argmax over this wave's batches ----
     // (first two batches issued here, once the layer weights are dead, so they
@@ -427,11 +589,11 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
 #pragma unroll
         for (int b = 0; b < LM_NBUF; ++b)
             if (b < lm_rounds) loadLM(lb[b], b);
-        __syncthreads();                                       // B1 (x of the last layer)
+        lds_barrier();                                         // B1 (x of the last layer)
         if (sm.abort) aborted = true;
     }
     if (!aborted) {
-        __syncthreads();                                       // B2 (final-normalized x)
+        lds_barrier();                                         // B2 (final-normalized x)
         uint32_t xp[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) xp[i] = sm.xp[lane][i];
@@ -460,7 +622,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     }
     best = wave_max_u64(best);
     if (lane == 0) sm.best[cw] = best;
-    __syncthreads();                                           // B6
+    lds_barrier();                                             // B6
 }
 
 }  // namespace dec
@@ -478,8 +640,9 @@ using namespace mq4;
 extern "C" size_t mq4_decode_workspace_size(int64_t hidden, int64_t intermediate, int64_t vocab) {
     (void)vocab;
     if (hidden <= 0 || intermediate <= 0) return 0;
-    // ctrl (256 B) + x words + h words + per-workgroup partial keys, each 256-byte aligned
-    const size_t xw = (size_t)hidden / 2 * 8, hw = (size_t)intermediate / 2 * 8;
+    // ctrl (256 B) + copies of the x and h words + per-workgroup partial
+    // keys, each 256-byte aligned
+    const size_t xw = (size_t)dec::kCopies * hidden / 2 * 8, hw = (size_t)dec::kCopies * intermediate / 2 * 8;
     auto up = [](size_t b) { return (b + 255) / 256 * 256; };
     return 256 + up(xw) + up(hw) + up((size_t)dec::kNWG * 8);
 }
@@ -513,7 +676,12 @@ extern "C" int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t int
             return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer in layer %lld", what, (long long)l);
         if (!aligned(s.norm_weight, 16) || !aligned(s.gate_wq, 16) || !aligned(s.up_wq, 16) ||
             !aligned(s.down_wq, 16))
-            return fail(MQ4_ERR_ALIGNMENT, "%s: layer %lld pointers must be 16-byte aligned", what, (long long)l);
+            return fail(MQ4_ERR_ALIGNMENT, "%s: layer %lld norm and packed weights must be 16-byte aligned", what,
+                        (long long)l);
+        if (!aligned(s.gate_scales, 4) || !aligned(s.gate_biases, 4) || !aligned(s.up_scales, 4) ||
+            !aligned(s.up_biases, 4) || !aligned(s.down_scales, 4) || !aligned(s.down_biases, 4))
+            return fail(MQ4_ERR_ALIGNMENT, "%s: layer %lld scales and biases must be 4-byte aligned", what,
+                        (long long)l);
         p.layers[l] = {s.norm_weight,
                        {s.gate_wq, s.gate_scales, s.gate_biases},
                        {s.up_wq, s.up_scales, s.up_biases},
@@ -540,7 +708,8 @@ extern "C" int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t int
     p.vocab = (int)vocab;
     p.n_layers = (int)n_layers;
     char* ws = reinterpret_cast<char*>(workspace);
-    const size_t xw = ((size_t)hidden / 2 * 8 + 255) / 256 * 256, hw = ((size_t)intermediate / 2 * 8 + 255) / 256 * 256;
+    const size_t xw = ((size_t)dec::kCopies * hidden / 2 * 8 + 255) / 256 * 256,
+                 hw = ((size_t)dec::kCopies * intermediate / 2 * 8 + 255) / 256 * 256;
     p.ctrl = reinterpret_cast<uint32_t*>(ws);
     p.xbuf = reinterpret_cast<uint64_t*>(ws + 256);
     p.hbuf = reinterpret_cast<uint64_t*>(ws + 256 + xw);

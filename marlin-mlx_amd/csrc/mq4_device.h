@@ -30,12 +30,16 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h) {
     return __uint_as_float(h << 16);
 }
 
-// float -> bf16 bits, round to nearest even; NaN becomes a quiet NaN.
+// float -> bf16 bits, round to nearest even; NaN becomes the quiet NaN
+// (bits >> 16) | 0x40.  gfx950's v_cvt_pk_bf16_f32 does exactly this (it is
+// bit-identical to the integer formulation, add 0x7fff + lsb then shift, with
+// that NaN rule, over all 2^32 inputs), one instruction for two values.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // Round to bf16 and back (the value a bf16 tensor would hold).
@@ -75,11 +79,25 @@ __device__ __forceinline__ uint32_t nib_pair_bf16(uint32_t word) {
 // Contribution of one 16-byte slice (32 K elements, half a group):
 // sum_k x_k*(s*q_k + b) = s*D + (b - 128*s)*X with D = sum_k x_k*(128 + q_k)
 // (the dot2 of the nibble pairs) and X = sum_k x_k.
-__device__ __forceinline__ float affine_term(uint32_t sbits, uint32_t bbits, float d, float xsum) {
+__device__ __forceinline__ float affine_c(float s, uint32_t bbits) {
 #pragma clang fp contract(off)
-    const float s = bf16_to_f32(sbits);
-    const float c = bf16_to_f32(bbits) - 128.0f * s;    // 128*s is exact
+    return bf16_to_f32(bbits) - 128.0f * s;    // 128*s is exact
+}
+__device__ __forceinline__ float affine_term_f(float s, float c, float d, float xsum) {
+#pragma clang fp contract(off)
     return __builtin_fmaf(s, d, c * xsum);
+}
+__device__ __forceinline__ float affine_term(uint32_t sbits, uint32_t bbits, float d, float xsum) {
+    const float s = bf16_to_f32(sbits);
+    return affine_term_f(s, affine_c(s, bbits), d, xsum);
+}
+
+// The four nibble pairs of one packed word (see nib_pair_bf16).
+__device__ __forceinline__ void nib_pairs(uint32_t word, uint32_t* out4) {
+    out4[0] = nib_pair_bf16<0>(word);
+    out4[1] = nib_pair_bf16<1>(word);
+    out4[2] = nib_pair_bf16<2>(word);
+    out4[3] = nib_pair_bf16<3>(word);
 }
 
 // s + lo^2 + hi^2 of one word holding two bf16 values.
@@ -99,9 +117,8 @@ __device__ __forceinline__ float rms_inv(float ss, int K, float eps) {
 // (src/model/marlin.cpp:12-16).
 __device__ __forceinline__ uint32_t norm_word(uint32_t x, uint32_t w, float r) {
 #pragma clang fp contract(off)
-    const uint32_t lo = f32_to_bf16(bf16_to_f32(x & 0xffffu) * r * (1.0f + bf16_to_f32(w & 0xffffu)));
-    const uint32_t hi = f32_to_bf16(bf16_to_f32(x >> 16) * r * (1.0f + bf16_to_f32(w >> 16)));
-    return lo | (hi << 16);
+    return f32x2_to_bf16x2(bf16_to_f32(x & 0xffffu) * r * (1.0f + bf16_to_f32(w & 0xffffu)),
+                           bf16_to_f32(x >> 16) * r * (1.0f + bf16_to_f32(w >> 16)));
 }
 
 // One 16-byte activation chunk (8 bf16 values in words a.x..a.w) -> the four
