@@ -56,6 +56,12 @@ KERNEL_BYTES = {                                  # algorithmic bytes per launch
 }
 
 
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (separate runs of
+# `bench.py --profile-kernel decode_step`), each scaled by the same counter's reading for a
+# 256 MiB device copy (FETCH x 1.99982, WRITE x 1.0); see profiles/decode_step_m1_hbm_traffic.md.
+MEASURED_TRAFFIC = {"decode_step": 803_470_292 + 6_299_750}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -69,6 +75,11 @@ def parse():
                    help="eager steps with per-kernel HIP events (roofline)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-reps", type=int, default=3)
+    p.add_argument("--profile-kernel", choices=["decode_step", "copy"], default=None,
+                   help="counter-collection mode: run only the one-launch decode step (warmup + steps "
+                        "launches) or, to calibrate FETCH_SIZE/WRITE_SIZE, a plain device copy of "
+                        "--copy-mib MiB per launch; prints no JSON line")
+    p.add_argument("--copy-mib", type=int, default=256)
     return p.parse_args()
 
 
@@ -97,6 +108,16 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     P = ctypes.c_void_p
+
+    if args.profile_kernel == "copy":
+        n = args.copy_mib * (1 << 20)
+        src = torch.ones(n // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy: {args.warmup + args.steps} launches of {n} bytes read + {n} bytes written")
+        return
 
     # ---------------------------------------------------------------- setup
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; generating + packing "
@@ -162,6 +183,18 @@ def main():
         return out
 
     steps = launches()
+
+    if args.profile_kernel == "decode_step":
+        qt = lambda q: mq4.QuantizedTensor(q.wq, q.s, q.b)
+        dec_layers = [mq4.DecoderLayer(layer_norms[l], mq4.MLPWeights(qt(g), qt(u), qt(d)))
+                      for l, (g, u, d) in enumerate(layers)]
+        dstep = mq4.DecodeStep(dec_layers, norm_w, qt(lm), EPS)
+        idx_p = torch.zeros((1,), dtype=torch.int32, device=dev)
+        for _ in range(args.warmup + args.steps):
+            dstep(x0, None, idx_p)
+        torch.cuda.synchronize()
+        log(f"[bench] decode_step: {args.warmup + args.steps} launches, token {int(idx_p.item())}")
+        return
 
     def run_step(st):
         for _, fn in steps:
@@ -249,7 +282,7 @@ def main():
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(dk["GBps"] / HBM_PEAK_GBPS, 4),
-        "traffic": None,
+        "traffic": MEASURED_TRAFFIC.get(dom),
     }
 
     # ------------------------------------ the whole step in one launch
@@ -328,7 +361,7 @@ def main():
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(dk["GBps"] / HBM_PEAK_GBPS, 4),
-        "traffic": None,
+        "traffic": MEASURED_TRAFFIC.get(dom),
     }
 
     # ------------------------------------------------------- CPU baseline
