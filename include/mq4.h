@@ -204,6 +204,7 @@ typedef struct mq4_mlp_layer {
     const uint32_t* down_wq; const uint16_t* down_scales; const uint16_t* down_biases;
 } mq4_mlp_layer;
 
+/* Bytes of workspace mq4_decode_step needs (0 for unsupported sizes). */
 size_t mq4_decode_workspace_size(int64_t hidden, int64_t intermediate, int64_t vocab);
 int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t intermediate, int64_t n_layers,
                     const mq4_mlp_layer* layers, const uint16_t* final_norm, float eps,

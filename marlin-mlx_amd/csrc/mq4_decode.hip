@@ -96,6 +96,10 @@ __device__ __forceinline__ void set_error(uint32_t* ctrl) {
 
 // Poll NW tagged words starting at src (NW a multiple of 64) until every tag
 // equals `tag`; store the 2*NW bf16 values to dst.  false on timeout/abort.
+// One round in flight: a second, staggered round doubles the poll traffic,
+// and all polls slow down by more than the finer sampling gains.  (Packing
+// three bf16 and a 16-bit tag per word measured slower too: the scattered
+// 16-bit LDS unpack costs more than the saved poll bytes.)
 template <int NW>
 __device__ bool poll_words(const uint64_t* src, uint32_t tag, uint32_t* dst, const Params& p, int lane) {
     constexpr int PER = NW / 64;
@@ -121,15 +125,6 @@ __device__ bool poll_words(const uint64_t* src, uint32_t tag, uint32_t* dst, con
 #pragma unroll
     for (int i = 0; i < PER; ++i) dst[i * 64 + lane] = (uint32_t)w[i];
     return true;
-}
-
-// Pair one slice (16 words = 32 bf16 values) for dot2 and sum its values, in
-// the order of the separate kernels: X = (((0 + c0) + c1) + c2) + c3.
-__device__ __forceinline__ void pair_slice(const uint32_t* words, uint32_t* out16, float* sum) {
-    float s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) s = pair_chunk(reinterpret_cast<const uint4*>(words)[w], out16 + 4 * w, s);
-    *sum = s;
 }
 
 // Per-compute-wave LDS staging of one layer's weights (filled by LDS DMA):
@@ -165,10 +160,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 struct alignas(16) Smem {
     uint32_t xraw[H / 2];          // raw x of the current layer (residual), bf16 pairs
-    uint32_t xp[SA][16];           // dot2-paired normalized x per slice
+    uint4 xp[4][SA];               // dot2-paired normalized x: chunk w of slice s at [w][s]
     float xs[SA];
     uint32_t hraw[I / 2];          // h as polled
-    uint32_t hp[SB][16];           // dot2-paired h per slice
+    uint4 hp[4][SB];               // dot2-paired h, same chunk-major layout (conflict-free reads)
     float hs[SB];
     uint32_t out[32];              // this workgroup's outputs (bf16 in the low half)
     uint64_t best[kNCW];
@@ -223,17 +218,26 @@ __device__ void stage_norm_x(Smem& sm, const uint4 nw, float eps, int io, int la
                                 norm_word(xv.w, nw.w, r));
     uint32_t pr[4];
     const float c = pair_chunk(xn, pr, 0.0f);
-    *reinterpret_cast<uint4*>(&sm.xp[sl][4 * q]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    sm.xp[q][sl] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
     const float c1 = quad_lane<1>(c), c2 = quad_lane<2>(c), c3 = quad_lane<3>(c);
     if (q == 0) sm.xs[sl] = ((c + c1) + c2) + c3;
 }
 
-// Pair the polled h (this wave's quarter of the slices).
+// Pair the polled h (this wave's quarter of the slices): 4 lanes per slice,
+// one 16-byte chunk each.  The slice sum ((c0 + c1) + c2) + c3 of the chunk
+// sums c = 0 + C equals the separate kernels' (((0 + C0) + C1) + C2) + C3 (no
+// partial sum can be -0, so the extra + 0 never changes a bit).
 __device__ void stage_h(Smem& sm, int io, int lane) {
-    constexpr int SPW = SB / kNIO;    // 48 slices per wave
-    for (int s = lane; s < SPW; s += 64) {
-        const int sl = io * SPW + s;
-        pair_slice(&sm.hraw[sl * 16], sm.hp[sl], &sm.hs[sl]);
+    constexpr int SPW = SB / kNIO;    // 48 slices per wave, 16 per pass
+    const int q = lane & 3;
+#pragma unroll
+    for (int pass = 0; pass < SPW / 16; ++pass) {
+        const int sl = io * SPW + pass * 16 + (lane >> 2);
+        uint32_t pr[4];
+        const float c = pair_chunk(reinterpret_cast<const uint4*>(sm.hraw)[sl * 4 + q], pr, 0.0f);
+        sm.hp[q][sl] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        const float c1 = quad_lane<1>(c), c2 = quad_lane<2>(c), c3 = quad_lane<3>(c);
+        if (q == 0) sm.hs[sl] = ((c + c1) + c2) + c3;
     }
 }
 
@@ -526,7 +530,10 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         {
             uint32_t xp[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) xp[i] = sm.xp[lane][i];
+            for (int w = 0; w < 4; ++w) {
+                const uint4 c = sm.xp[w][lane];
+                xp[4 * w] = c.x, xp[4 * w + 1] = c.y, xp[4 * w + 2] = c.z, xp[4 * w + 3] = c.w;
+            }
             const float xs = sm.xs[lane];
             float acc[2 * RA + 2];   // value index v = r*2 + t; padded to 8 values
 #pragma unroll
@@ -556,7 +563,10 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
                 const int sl = j * 64 + lane;
                 uint32_t hp[16];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) hp[i] = sm.hp[sl][i];
+                for (int w = 0; w < 4; ++w) {
+                    const uint4 c = sm.hp[w][sl];
+                    hp[4 * w] = c.x, hp[4 * w + 1] = c.y, hp[4 * w + 2] = c.z, hp[4 * w + 3] = c.w;
+                }
                 acc[j] += affine_term_f(ks_b[j], kc_b[j], pairs_d(pb[j], hp), sm.hs[sl]);
             }
             const float v = wave_multi_reduce<4>(acc, lane);    // lane >> 4 = third
@@ -596,7 +606,10 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         lds_barrier();                                         // B2 (final-normalized x)
         uint32_t xp[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) xp[i] = sm.xp[lane][i];
+        for (int w = 0; w < 4; ++w) {
+            const uint4 c = sm.xp[w][lane];
+            xp[4 * w] = c.x, xp[4 * w + 1] = c.y, xp[4 * w + 2] = c.z, xp[4 * w + 3] = c.w;
+        }
         const float xs = sm.xs[lane];
         auto consume = [&](LmBuf& B, int round) {
             float acc[LM_RPI];
@@ -639,7 +652,7 @@ using namespace mq4;
 
 extern "C" size_t mq4_decode_workspace_size(int64_t hidden, int64_t intermediate, int64_t vocab) {
     (void)vocab;
-    if (hidden <= 0 || intermediate <= 0) return 0;
+    if (hidden != dec::H || intermediate != dec::I) return 0;
     // ctrl (256 B) + copies of the x and h words + per-workgroup partial
     // keys, each 256-byte aligned
     const size_t xw = (size_t)dec::kCopies * hidden / 2 * 8, hw = (size_t)dec::kCopies * intermediate / 2 * 8;

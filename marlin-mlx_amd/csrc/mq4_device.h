@@ -192,6 +192,10 @@ __device__ __forceinline__ float lane_value(float v, int src) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
+__device__ __forceinline__ uint32_t lane_bits(uint32_t v, int src) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, src);
+}
+
 // Value of lane K of this lane's quad (DPP quad_perm broadcast).
 template <int K>
 __device__ __forceinline__ float quad_lane(float v) {
