@@ -56,7 +56,7 @@ constexpr int SPL_B = SB / 64;       // down slices per lane (3)
 constexpr int RA = I / kNWG / kNCW;  // gate/up rows per compute wave (3)
 constexpr int RB = H / kNWG / kNCW;  // down rows per compute wave (1)
 constexpr int LM_RPI = 4;            // lm_head rows per batch
-constexpr int LM_NBUF = 2;           // lm_head batches in flight per compute wave
+constexpr int LM_NBUF = 3;           // lm_head batches in flight per compute wave
 static_assert(SA == 64 && SB % 64 == 0 && RA * kNWG * kNCW == I && RB * kNWG * kNCW == H, "shape");
 
 struct Layer {

@@ -30,6 +30,7 @@
 //    K-split waves of a wave group through LDS.  A block holds NG independent
 //    wave groups.
 #include "mq4_device.h"
+#include "mq4_gemm.h"
 #include "mq4_host.h"
 
 namespace mq4 {
@@ -525,6 +526,13 @@ static int check_norm(const char* what, const uint16_t* norm_w, float eps) {
     return MQ4_OK;
 }
 
+// From kGemmMinM rows on, the entry points use the MFMA GEMM of mq4_gemm.hip
+// (weights read once per 128-row tile instead of once per 4 rows).
+static int run_gemm(const GemvParams& a, int64_t M, int epi, hipStream_t st) {
+    GemmArgs g{a.x, (int)M, a.N, a.K, a.A, a.B, a.y, a.res};
+    return launch_q4_gemm(g, epi, st);
+}
+
 static GemvParams params(const uint16_t* x, int64_t M, int64_t K, int64_t N, QMat A, QMat B, uint16_t* y) {
     GemvParams a{};
     a.x = x;
@@ -550,6 +558,10 @@ static int gate_up_impl(const char* what, const uint16_t* x, int64_t M, int64_t 
     GemvParams a = params(x, M, K, N, {gate_wq, gate_scales, gate_biases}, {up_wq, up_scales, up_biases}, h);
     a.norm_w = norm_w;
     a.eps = eps;
+    if (!NORM && M >= kGemmMinM) {   // (the fused RMSNorm variant stays on the GEMV)
+        run_gemm(a, M, GEMM_SWIGLU, as_stream(stream));
+        return launch_status(what);
+    }
     if (run_gemv<EPI_SWIGLU, NORM>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
@@ -596,6 +608,10 @@ extern "C" int mq4_qmm(const uint16_t* x, int64_t M, int64_t K, const uint32_t* 
     if (int rc = check_qmm_args(what, x, M, K, wq, scales, biases, N)) return rc;
     if (!y || !aligned(y, 2)) return fail(MQ4_ERR_INVALID_ARG, "%s: y must be a 2-byte aligned pointer", what);
     GemvParams a = params(x, M, K, N, {wq, scales, biases}, {nullptr, nullptr, nullptr}, y);
+    if (M >= kGemmMinM) {
+        run_gemm(a, M, GEMM_STORE, as_stream(stream));
+        return launch_status(what);
+    }
     if (run_gemv<EPI_STORE, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
@@ -609,6 +625,10 @@ extern "C" int mq4_qmm_f32(const uint16_t* x, int64_t M, int64_t K, const uint32
     if (!y || !aligned(y, 4)) return fail(MQ4_ERR_INVALID_ARG, "%s: y must be a 4-byte aligned pointer", what);
     GemvParams a = params(x, M, K, N, {wq, scales, biases}, {nullptr, nullptr, nullptr},
                           reinterpret_cast<uint16_t*>(y));
+    if (M >= kGemmMinM) {
+        run_gemm(a, M, GEMM_STORE_F32, as_stream(stream));
+        return launch_status(what);
+    }
     if (run_gemv<EPI_STORE_F32, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
@@ -623,6 +643,10 @@ extern "C" int mq4_qmm_residual(const uint16_t* x, int64_t M, int64_t K, const u
         return fail(MQ4_ERR_INVALID_ARG, "%s: y and residual must be 2-byte aligned pointers", what);
     GemvParams a = params(x, M, K, N, {wq, scales, biases}, {nullptr, nullptr, nullptr}, y);
     a.res = residual;
+    if (M >= kGemmMinM) {
+        run_gemm(a, M, GEMM_RESIDUAL, as_stream(stream));
+        return launch_status(what);
+    }
     if (run_gemv<EPI_RESIDUAL, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);

@@ -1,0 +1,132 @@
+"""Large-M Q4 GEMM (bf16 MFMA, weights dequantized into LDS) through the C ABI.
+
+From M = 33 rows on, mq4_qmm / mq4_qmm_f32 / mq4_qmm_residual /
+mq4_mlp_gate_up_silu run the MFMA GEMM (prefill: the prompt's S tokens through
+qmatmul, src/model/marlin.cpp:18-25, and mlp_forward, :31-35).  Bars, against
+the oracle's fp64 product of the same bf16 inputs and Q4 weights:
+* fp32 output: max|err| <= 1e-2 x rms(ref) (measured ~1e-5: each dequantized
+  weight enters the MFMA as a bf16 hi + lo pair, ~2^-17 relative);
+* bf16 output: the fp32 bar plus the output's own rounding, half a bf16 ulp
+  of |ref|, and >= 98% bit-identical to bf16(ref);
+* fused SwiGLU: the GEMV's element-wise bar (check_swiglu): >= 99%
+  bit-identical to the oracle's bf16 op chain on the fp64 gate/up, the rest
+  within 8 bf16 ulps or 2^-8 rms (one ulp flip of g can move h by ~5 ulps
+  through bf16(sigmoid(g)));
+* residual: bf16(res + bf16(acc)) equals the same formula on the GEMM's own
+  fp32 product bit for bit.
+At the prefill sizes (M = 1960 / 2048 / 8192) the oracle checks a spread of
+rows; the others are covered by the row-independent kernel (every row runs
+the same code on its own data) and by the small ragged shapes.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev_bf16, to_host_u16
+from test_gpu_parity import check_swiglu
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def q_host(wq, s, b):
+    return wq.cpu().numpy().view(np.uint32), to_host_u16(s), to_host_u16(b)
+
+
+def make(mq4, O, N, K, sid, dev):
+    w = mq4.fill_normal_bf16((N, K), sid, 0.0, 0.02, device=dev)
+    wq, s, b = mq4.quantize(w)
+    return (wq, s, b), q_host(wq, s, b)
+
+
+def check_f32(got, ref64, what):
+    ref64 = np.asarray(ref64, np.float64)
+    rms = float(np.sqrt(np.mean(ref64 * ref64)))
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - ref64))) / rms
+    print(f"{what}: fp32 max|err|/rms = {err:.2e}")
+    assert err <= TOL, f"{what}: {err:.3e}"
+
+
+def check_bf16(O, got_bits, ref64, what):
+    ref64 = np.asarray(ref64, np.float64)
+    rms = float(np.sqrt(np.mean(ref64 * ref64)))
+    got = O.bf16_to_f32(got_bits).astype(np.float64)
+    allow = TOL * rms + np.abs(ref64) * 2.0 ** -9
+    bad = np.abs(got - ref64) > allow
+    same = float(np.mean(got_bits == O.f64_to_bf16(ref64)))
+    print(f"{what}: bf16 max|err|/rms = {float(np.max(np.abs(got - ref64))) / rms:.2e}, "
+          f"identical to bf16(ref) {same:.4f}")
+    assert not bad.any(), f"{what}: {int(bad.sum())} outputs beyond the bar"
+    assert same >= 0.98
+
+
+@pytest.mark.parametrize("M,N,K", [(33, 128, 64), (64, 256, 512), (130, 200, 2048), (257, 384, 1024),
+                                   (96, 6144, 2048), (40, 2048, 6144)])
+def test_gemm_qmm_small_against_fp64(mq4, O, dev, M, N, K):
+    print(f"gemm M={M} N={N} K={K}", flush=True)
+    (wq, s, b), qh = make(mq4, O, N, K, 1000 + N + K, dev)
+    xh = O.gen_normal_bf16(4000, M * K).reshape(M, K)
+    x = to_dev_bf16(xh, dev)
+    y32 = mq4.quantized_matmul_f32(x, wq, s, b)
+    y = mq4.quantized_matmul(x, wq, s, b)
+    torch.cuda.synchronize()
+    ref64, _ = O.qmm_f64(xh, *qh)
+    check_f32(y32.cpu().numpy(), ref64, f"M={M} N={N} K={K}")
+    check_bf16(O, to_host_u16(y), ref64, f"M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("M", [1960, 2048, 8192])
+def test_gemm_prefill_shapes_sampled_rows(mq4, O, dev, M):
+    """BASELINE prefill: M tokens through gate (6144x2048) and down (2048x6144)."""
+    print(f"prefill M={M}", flush=True)
+    rows = np.unique(np.concatenate([np.arange(0, M, max(1, M // 13)), [M - 1, M - 2, 127, 128]]))
+    for (N, K, sid) in [(6144, 2048, 1000), (2048, 6144, 1002)]:
+        (wq, s, b), qh = make(mq4, O, N, K, sid, dev)
+        x = mq4.fill_normal_bf16((M, K), mq4.STREAM_PREFILL, 0.0, 1.0, device=dev)
+        y32 = mq4.quantized_matmul_f32(x, wq, s, b)
+        torch.cuda.synchronize()
+        xs = to_host_u16(x)[rows]
+        ref64, _ = O.qmm_f64(xs, *qh)
+        check_f32(y32.cpu().numpy()[rows], ref64, f"prefill M={M} N={N} K={K}")
+
+
+def test_gemm_swiglu_and_residual(mq4, O, dev):
+    M, N, K = 200, 6144, 2048
+    (g, gh), (u, uh) = make(mq4, O, N, K, 1003, dev), make(mq4, O, N, K, 1004, dev)
+    xh = O.gen_normal_bf16(4001, M * K).reshape(M, K)
+    x = to_dev_bf16(xh, dev)
+    G = mq4.QuantizedTensor(*g)
+    U = mq4.QuantizedTensor(*u)
+    h = mq4.mlp_gate_up_silu(x, G, U)
+    torch.cuda.synchronize()
+    _, gb = O.qmm_f64(xh, *gh)
+    _, ub = O.qmm_f64(xh, *uh)
+    check_swiglu(O, to_host_u16(h), O.swiglu_bf16(gb, ub), "GEMM SwiGLU")
+
+    # residual epilogue: down projection of h, added to a residual stream
+    (d, dh) = make(mq4, O, K, N, 1005, dev)
+    D = mq4.QuantizedTensor(*d)
+    res = mq4.fill_normal_bf16((M, K), 3001, 0.0, 1.0, device=dev)
+    y = mq4.qmatmul_residual(h, D, res)
+    y32 = mq4.quantized_matmul_f32(h, *d)
+    torch.cuda.synchronize()
+    want = O.add_bf16(to_host_u16(res), O.f32_to_bf16(y32.cpu().numpy()))
+    assert np.array_equal(to_host_u16(y), want)
+    ref64, _ = O.qmm_f64(to_host_u16(h), *dh)
+    check_f32(y32.cpu().numpy(), ref64, "down")
+
+
+def test_gemm_and_gemv_agree_at_the_switch(mq4, O, dev):
+    """M = 32 runs the GEMV, M = 33 the GEMM: both rows-0..31 results are
+    within the bar of the same fp64 reference."""
+    N, K = 512, 2048
+    (wq, s, b), qh = make(mq4, O, N, K, 11, dev)
+    xh = O.gen_normal_bf16(4002, 33 * K).reshape(33, K)
+    x = to_dev_bf16(xh, dev)
+    a = mq4.quantized_matmul_f32(x[:32].contiguous(), wq, s, b)
+    c = mq4.quantized_matmul_f32(x, wq, s, b)
+    torch.cuda.synchronize()
+    ref64, _ = O.qmm_f64(xh, *qh)
+    check_f32(a.cpu().numpy(), ref64[:32], "GEMV M=32")
+    check_f32(c.cpu().numpy(), ref64, "GEMM M=33")
