@@ -10,7 +10,8 @@
  *          dequantizes to scales[n, k/64] * q + biases[n, k/64]
  *   x      bf16 [M, K] row-major; y bf16 [M, N] row-major
  * Only group_size 64 and bits 4 are implemented; other values return
- * MQ4_ERR_UNSUPPORTED.  K must be a positive multiple of 64.
+ * MQ4_ERR_UNSUPPORTED.  K must be a positive multiple of 64, at most 32768
+ * for the matrix products (larger K returns MQ4_ERR_UNSUPPORTED).
  *
  * All pointers are device pointers (hipMalloc'd or equivalent) and `stream`
  * is a hipStream_t (NULL = the default stream).  Every call is asynchronous

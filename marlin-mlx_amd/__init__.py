@@ -141,6 +141,51 @@ def _need(t: torch.Tensor, dtype, name: str) -> torch.Tensor:
     return t.contiguous()
 
 
+def _check_weight(fn: str, wq: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, K: int,
+                  group_size: int = GROUP_SIZE, bits: int = BITS) -> int:
+    """Shapes and dtypes of one MLX-layout quantized matrix against an input
+    of K features (what mx::quantized_matmul validates): wq int32 [N, K*bits/32],
+    scales and biases bf16 [N, K/group_size].  Returns N.  Checked before any
+    pointer reaches the C ABI, which only sees raw addresses."""
+    for t, name in ((wq, "weight"), (scales, "scales"), (biases, "biases")):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{fn}: {name} must be a torch.Tensor")
+    if wq.dtype != torch.int32:
+        raise TypeError(f"{fn}: packed weight must be int32 (uint32 words), got {wq.dtype}")
+    if scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+        raise TypeError(f"{fn}: scales and biases must be bfloat16")
+    if wq.dim() != 2:
+        raise ValueError(f"{fn}: packed weight must be 2-D [N, K/8], got shape {tuple(wq.shape)}")
+    if group_size <= 0 or bits <= 0 or K % group_size != 0 or (K * bits) % 32 != 0:
+        raise ValueError(f"{fn}: K={K} is not a multiple of group_size={group_size}")
+    N = wq.shape[0]
+    if wq.shape[1] != K * bits // 32:
+        raise ValueError(f"{fn}: input has K={K} features but the weight holds "
+                         f"{wq.shape[1] * 32 // bits} (shape {tuple(wq.shape)})")
+    want = (N, K // group_size)
+    if tuple(scales.shape) != want or tuple(biases.shape) != want:
+        raise ValueError(f"{fn}: scales/biases must be {want}, got {tuple(scales.shape)} and "
+                         f"{tuple(biases.shape)}")
+    return N
+
+
+def _check_vector(fn: str, t: torch.Tensor, n: int, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{fn}: {name} must be a torch.Tensor")
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{fn}: {name} must be bfloat16")
+    if t.numel() != n:
+        raise ValueError(f"{fn}: {name} must hold {n} values, got {t.numel()}")
+
+
+def _in_features(fn: str, x: torch.Tensor) -> int:
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{fn}: input must be a torch.Tensor")
+    if x.dim() == 0 or x.shape[-1] == 0:
+        raise ValueError(f"{fn}: input must have a non-empty last dimension")
+    return x.shape[-1]
+
+
 # ----------------------------------------------------------------- ops ---
 
 def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4):
@@ -184,11 +229,12 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
                      transpose: bool = True, group_size: int = 64, bits: int = 4) -> torch.Tensor:
     """mx::quantized_matmul(x, w, scales, biases, transpose, group_size, bits):
     x bf16 [..., K] @ dequant(w [N, K/8])^T -> bf16 [..., N]."""
+    N = _check_weight("quantized_matmul", w, scales, biases, _in_features("quantized_matmul", x),
+                      group_size, bits)
     x = _need(x, torch.bfloat16, "x")
     w = _need(w, torch.int32, "w")
     scales = _need(scales, torch.bfloat16, "scales")
     biases = _need(biases, torch.bfloat16, "biases")
-    N = w.shape[0]
     M, K, y = _mk(x, N)
     _check(lib().mq4_qmm(_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N, int(transpose),
                          group_size, bits, _ptr(y), _stream(x.device)))
@@ -198,11 +244,11 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
 def quantized_matmul_f32(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                          biases: torch.Tensor) -> torch.Tensor:
     """quantized_matmul with the fp32 accumulator returned unrounded (float32)."""
+    N = _check_weight("quantized_matmul_f32", w, scales, biases, _in_features("quantized_matmul_f32", x))
     x = _need(x, torch.bfloat16, "x")
     w = _need(w, torch.int32, "w")
     scales = _need(scales, torch.bfloat16, "scales")
     biases = _need(biases, torch.bfloat16, "biases")
-    N = w.shape[0]
     K = x.shape[-1]
     M = x.numel() // K
     y = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=x.device)
@@ -293,12 +339,16 @@ def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor
     """swiglu(qmatmul(x, gate), qmatmul(x, up)) in one pass over both weights;
     with norm_weight, x is first rms_norm'ed with the (1 + w) multiplier
     (src/model/marlin.cpp:141) inside the same kernel."""
-    _require_quantized(gate, "mlp_gate_up_silu")
-    _require_quantized(up, "mlp_gate_up_silu")
+    fn = "mlp_gate_up_silu"
+    _require_quantized(gate, fn)
+    _require_quantized(up, fn)
+    Kx = _in_features(fn, x)
+    N = _check_weight(fn, gate.weight, gate.scales, gate.biases, Kx, gate.group_size, gate.bits)
+    if _check_weight(fn, up.weight, up.scales, up.biases, Kx, up.group_size, up.bits) != N:
+        raise ValueError(f"{fn}: gate and up must have the same shape")
+    if norm_weight is not None:
+        _check_vector(fn, norm_weight, Kx, "norm_weight")
     x = _need(x, torch.bfloat16, "x")
-    N = gate.out_features
-    if up.out_features != N:
-        raise ValueError("mlp_gate_up_silu: gate and up must have the same shape")
     M, K, h = _mk(x, N)
     g = (_ptr(gate.weight), _ptr(gate.scales), _ptr(gate.biases))
     u = (_ptr(up.weight), _ptr(up.scales), _ptr(up.biases))
@@ -315,14 +365,18 @@ def qmatmul_residual(x: torch.Tensor, w: QuantizedTensor, residual: torch.Tensor
                      out: torch.Tensor | None = None) -> torch.Tensor:
     """residual + qmatmul(x, w) with bf16 rounding of both (src/model/marlin.cpp:142);
     out may be residual itself (in-place)."""
-    _require_quantized(w, "qmatmul_residual")
-    x = _need(x, torch.bfloat16, "x")
-    residual = _need(residual, torch.bfloat16, "residual")
-    N = w.out_features
+    fn = "qmatmul_residual"
+    _require_quantized(w, fn)
+    N = _check_weight(fn, w.weight, w.scales, w.biases, _in_features(fn, x), w.group_size, w.bits)
     K = x.shape[-1]
     M = x.numel() // K
-    if residual.numel() != M * N:
-        raise ValueError("qmatmul_residual: residual shape mismatch")
+    if not isinstance(residual, torch.Tensor) or residual.numel() != M * N:
+        raise ValueError(f"{fn}: residual must hold M*N = {M * N} values")
+    if out is not None and (not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16
+                            or out.numel() != M * N or not out.is_contiguous()):
+        raise ValueError(f"{fn}: out must be a contiguous bf16 tensor of M*N = {M * N} values")
+    x = _need(x, torch.bfloat16, "x")
+    residual = _need(residual, torch.bfloat16, "residual")
     y = out if out is not None else torch.empty_like(residual)
     _check(lib().mq4_qmm_residual(_ptr(x), M, K, _ptr(w.weight), _ptr(w.scales), _ptr(w.biases), N,
                                   _ptr(residual), _ptr(y), _stream(x.device)))
@@ -350,9 +404,13 @@ def lm_head_argmax(hidden: torch.Tensor, w: QuantizedTensor, return_logits: bool
     """Greedy next token of every row of `hidden`: argmax of the bf16 logits,
     fused with the lm_head product (marlin.cpp:161-169 + sampler.cpp:14-16);
     with norm_weight also the final rms_norm (marlin.cpp:145) in front."""
-    _require_quantized(w, "lm_head_argmax")
+    fn = "lm_head_argmax"
+    _require_quantized(w, fn)
+    Kx = _in_features(fn, hidden)
+    N = _check_weight(fn, w.weight, w.scales, w.biases, Kx, w.group_size, w.bits)
+    if norm_weight is not None:
+        _check_vector(fn, norm_weight, Kx, "norm_weight")
     hidden = _need(hidden, torch.bfloat16, "hidden")
-    N = w.out_features
     K = hidden.shape[-1]
     M = hidden.numel() // K
     idx = torch.empty(hidden.shape[:-1], dtype=torch.int32, device=hidden.device)
@@ -382,6 +440,7 @@ def sample_token(logits: torch.Tensor, temperature: float = 0.0) -> torch.Tensor
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """src/model/marlin.cpp:12-16: x * rsqrt(mean(x^2) + eps) * (1 + weight)."""
+    _check_vector("rms_norm", weight, _in_features("rms_norm", x), "weight")
     x = _need(x, torch.bfloat16, "x")
     weight = _need(weight, torch.bfloat16, "weight")
     K = x.shape[-1]
@@ -432,24 +491,42 @@ class DecodeStep:
 
     def __init__(self, layers: list[DecoderLayer], final_norm: torch.Tensor, lm: QuantizedTensor,
                  eps: float = 1e-6):
-        _require_quantized(lm, "DecodeStep")
+        fn = "DecodeStep"
+        _require_quantized(lm, fn)
         self.layers = list(layers)
-        self.final_norm = _need(final_norm, torch.bfloat16, "final_norm")
+        self.hidden = lm.in_features
+        _check_weight(fn, lm.weight, lm.scales, lm.biases, self.hidden, lm.group_size, lm.bits)
+        _check_vector(fn, final_norm, self.hidden, "final_norm")
         self.lm = lm
         self.eps = float(eps)
-        self.hidden = lm.in_features
         self.intermediate = self.layers[0].mlp.gate_proj.out_features if self.layers else 6144
+        H, I = self.hidden, self.intermediate
+        # every pointer handed to the kernel is checked first: shapes and
+        # dtypes of all layers, then device and contiguity
+        for i, ly in enumerate(self.layers):
+            m = ly.mlp
+            for w, k, n, name in ((m.gate_proj, H, I, "gate_proj"), (m.up_proj, H, I, "up_proj"),
+                                  (m.down_proj, I, H, "down_proj")):
+                _require_quantized(w, fn)
+                if _check_weight(f"{fn} layer {i} {name}", w.weight, w.scales, w.biases, k,
+                                 w.group_size, w.bits) != n:
+                    raise ValueError(f"{fn}: layer {i} {name} must have {n} rows")
+            _check_vector(f"{fn} layer {i}", ly.post_attn_norm, H, "post_attn_norm")
         arr = (_MlpLayerC * max(1, len(self.layers)))()
         for i, ly in enumerate(self.layers):
             m = ly.mlp
-            for w in (m.gate_proj, m.up_proj, m.down_proj):
-                _require_quantized(w, "DecodeStep")
-            arr[i] = _MlpLayerC(ly.post_attn_norm.data_ptr(), m.gate_proj.weight.data_ptr(),
-                                m.gate_proj.scales.data_ptr(), m.gate_proj.biases.data_ptr(),
-                                m.up_proj.weight.data_ptr(), m.up_proj.scales.data_ptr(),
-                                m.up_proj.biases.data_ptr(), m.down_proj.weight.data_ptr(),
-                                m.down_proj.scales.data_ptr(), m.down_proj.biases.data_ptr())
+            tensors = [(ly.post_attn_norm, "post_attn_norm")]
+            for w, name in ((m.gate_proj, "gate_proj"), (m.up_proj, "up_proj"), (m.down_proj, "down_proj")):
+                tensors += [(w.weight, f"{name}.weight"), (w.scales, f"{name}.scales"), (w.biases, f"{name}.biases")]
+            for t, tn in tensors:
+                if not t.is_cuda or not t.is_contiguous():
+                    raise ValueError(f"{fn}: layer {i} {tn} must be a contiguous device tensor")
+            arr[i] = _MlpLayerC(*[t.data_ptr() for t, _ in tensors])
         self._arr = arr
+        self.final_norm = _need(final_norm, torch.bfloat16, "final_norm")
+        for t, tn in ((lm.weight, "weight"), (lm.scales, "scales"), (lm.biases, "biases")):
+            if not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{fn}: lm_head {tn} must be a contiguous device tensor")
         L = lib()
         self.ws_bytes = L.mq4_decode_workspace_size(self.hidden, self.intermediate, lm.out_features)
         self.workspace = torch.zeros(self.ws_bytes, dtype=torch.uint8, device=self.final_norm.device)

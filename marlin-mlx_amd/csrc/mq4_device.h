@@ -59,14 +59,10 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 template <int P>
 __device__ __forceinline__ uint32_t nib_pair_bf16(uint32_t word) {
     const uint32_t s = P ? (word >> (4 * P)) : word;
-#ifdef NO_ANDOR
-    return (s & 0x000F000Fu) | 0x43004300u;
-#else
     uint32_t m, c;
     asm("s_mov_b32 %0, 0x000f000f" : "=s"(m));
     asm("v_mov_b32 %0, 0x43004300" : "=v"(c));
     return (s & m) | c;
-#endif
 }
 
 // ---- per-element arithmetic shared by every decode kernel ----

@@ -38,6 +38,11 @@ namespace mq4 {
 enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3, EPI_STORE_F32 = 4 };
 
 constexpr int kPartialStride = 4096;     // max blocks of an argmax launch
+// Largest K the entry points accept: 1024 16-byte slices per row, two per
+// lane of eight K-split waves (the M = 1 instance; 4-row chunks of x switch
+// to single rows above K = 16384).  Larger K would need more slices per lane
+// than the register file holds without spilling.
+constexpr int kMaxK = 32768;
 
 struct GemvParams {
     const uint16_t* x;       // [m_valid, K]
@@ -474,7 +479,6 @@ static int dispatch_k(const GemvParams& a, hipStream_t st) {
     if (L <= 512) { launch_gemv<M, 1, 8, EPI, NORM>(a, st); return 0; }
     if constexpr (M == 1) {
         if (L <= 1024) { launch_gemv<M, 2, 8, EPI, NORM>(a, st); return 0; }
-        if (L <= 2048) { launch_gemv<M, 4, 8, EPI, NORM>(a, st); return 0; }
     }
     return -1;
 }
@@ -508,9 +512,9 @@ static int check_qmm_args(const char* what, const uint16_t* x, int64_t M, int64_
     if (M <= 0 || N <= 0)
         return fail(MQ4_ERR_INVALID_ARG, "%s: M=%lld and N=%lld must be positive", what, (long long)M,
                     (long long)N);
-    if (K > 65536)
-        return fail(MQ4_ERR_UNSUPPORTED, "%s: K=%lld exceeds the supported maximum 65536", what,
-                    (long long)K);
+    if (K > kMaxK)
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: K=%lld exceeds the supported maximum %d", what,
+                    (long long)K, kMaxK);
     if (N > 0x7fffffffLL) return fail(MQ4_ERR_UNSUPPORTED, "%s: N too large", what);
     if (!x || !wq || !s || !b) return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
     if (!aligned(x, 16) || !aligned(wq, 16) || !aligned(s, 2) || !aligned(b, 2))

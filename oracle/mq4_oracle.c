@@ -31,9 +31,29 @@
  *                         (src/sampling/sampler.cpp:14-16): strict '>' scan, the
  *                         first index wins ties.
  *   mq4o_rmsnorm_1pw      x * rsqrt(mean(x^2) + eps) * (1 + w)
- *                         (src/model/marlin.cpp:12-16), computed in fp32 and
- *                         rounded once to bf16 (input synthesis for the lm_head
- *                         workload, not a parity target).
+ *                         (src/model/marlin.cpp:12-16) with the sum of squares
+ *                         in fp64, r = 1/sqrtf(mean + eps) and (x*r)*(1+w) in
+ *                         fp32, one bf16 rounding: the formula the HIP kernels
+ *                         implement (their sum of squares is fp32), and the
+ *                         parity target for the fused norm entry points.
+ *   mq4o_rmsnorm_mlx      the same rms_norm as the chain of MLX ops it is
+ *                         written as (square, mean, + eps, rsqrt, *, 1 + w, *),
+ *                         each op producing an array of its MLX result dtype:
+ *                         square and mean of a bf16 array are bf16 (mean =
+ *                         bf16(sum) * bf16(1/K)); the float scalars eps and
+ *                         1.0f are float32 arrays in MLX's C++ API, so from
+ *                         "+ eps" on the chain is float32 (flag
+ *                         MQ4O_NORM_BF16_OPS instead keeps every op in bf16, the
+ *                         reading in which scalars do not promote).  The sum
+ *                         inside mean accumulates in fp32 (flag
+ *                         MQ4O_NORM_BF16_SUM: a bf16 accumulator, rounded after
+ *                         every add).  The float32 result is rounded once to
+ *                         bf16, the activation type of this path.  Used to
+ *                         bound how far the kernels' formula is from the
+ *                         reference's op order (which MLX itself, absent here,
+ *                         would fix).
+ *   mq4o_add_bf16         hidden + mlp(...) (src/model/marlin.cpp:142) on two
+ *                         bf16 arrays: bf16(a + b).
  *   mq4o_gen_normal_bf16  the synthetic-input generator (SplitMix64 counter
  *                         stream -> Box-Muller in fp64 -> mu + sigma*z -> bf16
  *                         round-to-nearest-even directly from fp64).
@@ -43,10 +63,17 @@
  * the edge element reconstructs exactly) and a brute-force exact-rational
  * nearest-level check; qmm_f64 by exact Fraction arithmetic on tiny shapes and
  * numpy's float64 dot; argmax by numpy.argmax; bf16 rounding by torch's
- * float->bfloat16 cast; the generator by a committed SHA-256 fixture.
+ * float->bfloat16 cast; the generator by a committed SHA-256 fixture;
+ * rmsnorm_1pw by exact known answers on tiny rows (each failing a misplaced
+ * eps, a w in place of 1 + w or a mean over the wrong count) and by an
+ * independent float64 formula on random rows; rmsnorm_mlx by torch's bf16 and
+ * float32 CPU ops replaying the same chain; add_bf16 by torch's bf16 add and by
+ * exact rationals.
  * Parity unpinned (needs a run of MLX itself, absent here): the tie-rounding
- * mode MLX uses inside quantize, MLX's bf16 accumulation order in _qmm_t, and
- * the exact bf16 bit pattern of MLX's sigmoid.
+ * mode MLX uses inside quantize, MLX's bf16 accumulation order in _qmm_t, the
+ * exact bf16 bit pattern of MLX's sigmoid, and which rms_norm chain (dtype
+ * promotion of the scalars, accumulator of the sum) MLX evaluates; the tests
+ * bound the distance between the kernels' formula and each reading instead.
  */
 #include <math.h>
 #include <omp.h>
@@ -355,6 +382,45 @@ void mq4o_rmsnorm_1pw(const uint16_t* x, const uint16_t* w, int64_t M, int64_t K
         float r = 1.0f / sqrtf((float)(ss / (double)K) + eps);
         for (int64_t k = 0; k < K; ++k)
             out[m * K + k] = f32_to_bf16(bf16_to_f32(xr[k]) * r * (1.0f + bf16_to_f32(w[k])));
+    }
+}
+
+/* rms_norm as the MLX op chain of src/model/marlin.cpp:12-16 (see the header
+ * for the two readings selected by the flags). */
+#define MQ4O_NORM_BF16_SUM 1
+#define MQ4O_NORM_BF16_OPS 2
+void mq4o_rmsnorm_mlx(const uint16_t* x, const uint16_t* w, int64_t M, int64_t K, float eps, int flags,
+                      uint16_t* out) {
+    const uint16_t inv_k = f32_to_bf16(1.0f / (float)K);        /* array(1.0 / n, bf16) */
+    for (int64_t m = 0; m < M; ++m) {
+        const uint16_t* xr = x + m * K;
+        float sumf = 0.0f;
+        uint16_t sumb = 0;
+        for (int64_t k = 0; k < K; ++k) {
+            float v = bf16_to_f32(xr[k]);
+            uint16_t sq = f32_to_bf16(v * v);                    /* square: bf16 */
+            if (flags & MQ4O_NORM_BF16_SUM) sumb = f32_to_bf16(bf16_to_f32(sumb) + bf16_to_f32(sq));
+            else sumf += bf16_to_f32(sq);
+        }
+        uint16_t sum = (flags & MQ4O_NORM_BF16_SUM) ? sumb : f32_to_bf16(sumf);   /* sum: bf16 */
+        uint16_t mean = f32_to_bf16(bf16_to_f32(sum) * bf16_to_f32(inv_k));       /* mean: bf16 */
+        if (flags & MQ4O_NORM_BF16_OPS) {
+            uint16_t v = f32_to_bf16(bf16_to_f32(mean) + bf16_to_f32(f32_to_bf16(eps)));
+            uint16_t r = f32_to_bf16(1.0f / sqrtf(bf16_to_f32(v)));
+            for (int64_t k = 0; k < K; ++k) {
+                uint16_t t = f32_to_bf16(bf16_to_f32(xr[k]) * bf16_to_f32(r));
+                uint16_t w1 = f32_to_bf16(1.0f + bf16_to_f32(w[k]));
+                out[m * K + k] = f32_to_bf16(bf16_to_f32(t) * bf16_to_f32(w1));
+            }
+        } else {
+            float v = bf16_to_f32(mean) + eps;                     /* float32 from here on */
+            float r = 1.0f / sqrtf(v);
+            for (int64_t k = 0; k < K; ++k) {
+                float t = bf16_to_f32(xr[k]) * r;
+                float w1 = 1.0f + bf16_to_f32(w[k]);
+                out[m * K + k] = f32_to_bf16(t * w1);
+            }
+        }
     }
 }
 

@@ -50,6 +50,7 @@ def lib():
         L.mq4o_swiglu_bf16.argtypes = [P, P, I64, P]
         L.mq4o_argmax_bf16.argtypes = [P, I64, I64, P]
         L.mq4o_rmsnorm_1pw.argtypes = [P, P, I64, I64, ctypes.c_float, P]
+        L.mq4o_rmsnorm_mlx.argtypes = [P, P, I64, I64, ctypes.c_float, ctypes.c_int, P]
         L.mq4o_add_bf16.argtypes = [P, P, I64, P]
         L.mq4o_f32_to_bf16_array.argtypes = [P, P, I64]
         L.mq4o_f64_to_bf16_array.argtypes = [P, P, I64]
@@ -174,6 +175,24 @@ def rmsnorm_1pw(x, w, eps: float = 1e-6):
     w = np.ascontiguousarray(w, dtype=np.uint16)
     out = np.empty((M, K), np.uint16)
     lib().mq4o_rmsnorm_1pw(_p(x), _p(w), M, K, eps, _p(out))
+    return out
+
+
+NORM_BF16_SUM = 1   # mean's sum accumulates in bf16 (rounded after every add)
+NORM_BF16_OPS = 2   # every op of the chain returns bf16 (scalars do not promote)
+
+
+def rmsnorm_mlx(x, w, eps: float = 1e-6, flags: int = 0):
+    """rms_norm (src/model/marlin.cpp:12-16) evaluated as its chain of MLX ops;
+    flags 0 = MLX C++ promotion (bf16 square/mean, float32 from + eps on,
+    fp32 sum), see mq4_oracle.c for the flag meanings."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    if x.ndim == 1:
+        x = x[None, :]
+    M, K = x.shape
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    out = np.empty((M, K), np.uint16)
+    lib().mq4o_rmsnorm_mlx(_p(x), _p(w), M, K, eps, flags, _p(out))
     return out
 
 

@@ -68,7 +68,7 @@ def test_qmm_validation(mq4):
     assert "transpose" in last_error(mq4)
     assert L.mq4_qmm(*args(g=128)) == UNSUPPORTED
     assert L.mq4_qmm(*args(K=100)) == INVALID
-    assert L.mq4_qmm(*args(K=65536 + 64)) == UNSUPPORTED
+    assert L.mq4_qmm(*args(K=32768 + 64)) == UNSUPPORTED
     assert L.mq4_qmm(*args(M=0)) == INVALID
     assert L.mq4_qmm(*args(N=0)) == INVALID
     assert L.mq4_qmm(*args(x=fake(A16 + 2))) == ALIGN

@@ -1,0 +1,129 @@
+"""Batched decode (M concurrent token rows, BASELINE config 5a) on the model's
+shapes through the C ABI, against the oracle on the same seeded inputs:
+
+* fused gate/up + SwiGLU (6144x2048), with and without the (1 + w) RMSNorm
+  in front (src/model/marlin.cpp:27-33, 141): element-wise SwiGLU bar of
+  check_swiglu against the oracle's bf16 op chain on bf16(fp64) g and u;
+* down + residual (2048x6144, src/model/marlin.cpp:34, 142): the fp32 product
+  within 1e-2 x rms of fp64 (the GEMV bar); the residual output equal to
+  bf16(residual + the kernel's own bf16 product) bit for bit, and within
+  2^-7 (|bf16(fp64)| + |ref|) + 2^-12 rms of ref = bf16(residual + bf16(fp64));
+* lm_head + greedy argmax over the full 248,320-row vocab
+  (src/model/marlin.cpp:161-169, src/sampling/sampler.cpp:14-16): logits
+  >= 98% identical to bf16(fp64), indices bit-exact on the kernel's own
+  logits and equal to the fp64 argmax unless the top two are within 1 ulp.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev_bf16, to_host_u16
+from test_gpu_parity import TOL, check_close, check_swiglu, rel_err_f32
+
+pytestmark = pytest.mark.gpu
+
+H, I, V = 2048, 6144, 248320
+MS = [16, 32]
+
+
+def q_host(qt):
+    return qt.weight.cpu().numpy().view(np.uint32), to_host_u16(qt.scales), to_host_u16(qt.biases)
+
+
+@pytest.fixture(scope="module")
+def mlp(mq4, dev):
+    ws = [mq4.quantize_weight(mq4.fill_normal_bf16((I, H) if p < 2 else (H, I), mq4.stream_id_layer(0, p),
+                                                   0.0, 0.02, device=dev)) for p in range(3)]
+    torch.cuda.synchronize()
+    return ws, [q_host(w) for w in ws]
+
+
+@pytest.mark.parametrize("M", MS)
+@pytest.mark.parametrize("norm", [False, True])
+def test_batched_gate_up_silu(mq4, O, dev, mlp, M, norm):
+    print(f"batched gate/up M={M} norm={norm}", flush=True)
+    (g, u, _), (gh, uh, _) = mlp
+    xh = O.gen_normal_bf16(3000, M * H, 0.0, 1.5).reshape(M, H)
+    nwh = O.gen_normal_bf16(2100, H, 0.1, 0.02)
+    x = to_dev_bf16(xh, dev)
+    h = mq4.mlp_gate_up_silu(x, g, u, norm_weight=to_dev_bf16(nwh, dev) if norm else None, eps=1e-6)
+    torch.cuda.synchronize()
+    n = O.rmsnorm_1pw(xh, nwh, 1e-6) if norm else xh
+    _, gb = O.qmm_f64(n, *gh)
+    _, ub = O.qmm_f64(n, *uh)
+    check_swiglu(O, to_host_u16(h), O.swiglu_bf16(gb, ub), f"gate/up M={M} norm={norm}")
+
+
+@pytest.mark.parametrize("M", MS)
+def test_batched_down_residual(mq4, O, dev, mlp, M):
+    print(f"batched down M={M}", flush=True)
+    (_, _, d), (_, _, dh) = mlp
+    hh = O.gen_normal_bf16(3100, M * I, 0.0, 0.3).reshape(M, I)
+    rh = O.gen_normal_bf16(3200, M * H).reshape(M, H)
+    hd = to_dev_bf16(hh, dev)
+    y = mq4.qmatmul_residual(hd, d, to_dev_bf16(rh, dev))
+    y32 = mq4.quantized_matmul_f32(hd, d.weight, d.scales, d.biases)
+    yq = mq4.qmatmul(hd, d)
+    torch.cuda.synchronize()
+    y64, yb = O.qmm_f64(hh, *dh)
+    check_close(O, to_host_u16(yq), y64, f"down M={M}", y32.cpu().numpy())
+    # the residual epilogue adds the bf16-rounded product of the same kernel family
+    want = O.add_bf16(rh, to_host_u16(yq))
+    assert np.array_equal(to_host_u16(y), want)
+    # against the oracle: the product's error (<= 2 ulps of bf16(fp64), see
+    # check_close) plus the sum's own rounding, in absolute terms (a sum that
+    # cancels to near zero makes an ulp count meaningless)
+    ref = O.add_bf16(rh, yb)
+    err = np.abs(O.bf16_to_f32(to_host_u16(y)).astype(np.float64) - O.bf16_to_f32(ref))
+    rms = float(np.sqrt(np.mean(y64 * y64)))
+    # |yq - yb| <= 2^-7 |yb| + fp32 noise; the two sums round apart by <= 1 ulp
+    allow = 2.0 ** -7 * np.abs(O.bf16_to_f32(yb)) + 2.0 ** -7 * np.abs(O.bf16_to_f32(ref)) + 2.0 ** -12 * rms
+    worst = np.unravel_index(np.argmax(err - allow), err.shape)
+    assert np.all(err <= allow), (f"at {worst}: y={O.bf16_to_f32(to_host_u16(y))[worst]} ref={O.bf16_to_f32(ref)[worst]} "
+                                  f"yq={O.bf16_to_f32(to_host_u16(yq))[worst]} yb={O.bf16_to_f32(yb)[worst]}")
+
+
+@pytest.fixture(scope="module")
+def lm(mq4, dev):
+    qt = mq4.quantize_weight(mq4.fill_normal_bf16((V, H), mq4.STREAM_LM_HEAD, 0.0, 0.02, device=dev))
+    torch.cuda.synchronize()
+    return qt, q_host(qt)
+
+
+@pytest.mark.parametrize("M", MS)
+def test_batched_lm_head_argmax(mq4, O, dev, lm, M):
+    print(f"batched lm_head M={M}", flush=True)
+    qt, qh = lm
+    xh = O.gen_normal_bf16(3300, M * H, 0.0, 3.0).reshape(M, H)
+    nwh = O.gen_normal_bf16(2001, H, 0.1, 0.02)
+    idx, logits = mq4.lm_head_argmax(to_dev_bf16(xh, dev), qt, return_logits=True,
+                                     norm_weight=to_dev_bf16(nwh, dev), eps=1e-6)
+    torch.cuda.synchronize()
+    hn = O.rmsnorm_1pw(xh, nwh, 1e-6)
+    ref64, refb = O.qmm_f64(hn, *qh)
+    lg = to_host_u16(logits)
+    ulp = O.bf16_ulp_diff(lg, refb)
+    print(f"lm_head M={M}: identical={np.mean(ulp == 0):.5f} max_ulp={int(ulp.max())}")
+    assert np.mean(ulp == 0) >= 0.98
+    rms = float(np.sqrt(np.mean(ref64 * ref64)))
+    assert np.max(np.abs(O.bf16_to_f32(lg).astype(np.float64) - ref64)) <= TOL * rms + np.abs(ref64).max() * 2.0 ** -8
+    got = idx.cpu().numpy().astype(np.uint32)
+    assert np.array_equal(got, O.argmax_bf16(lg))
+    want = O.argmax_bf16(refb)
+    for m in range(M):
+        if got[m] != want[m]:
+            top = np.sort(O.bf16_to_f32(refb[m]))[-2:]
+            assert O.bf16_ulp_diff(O.f32_to_bf16(top[:1]), O.f32_to_bf16(top[1:]))[0] <= 1, f"row {m}"
+
+
+@pytest.mark.parametrize("M", MS)
+def test_batched_qmm_f32_bar(mq4, O, dev, mlp, M):
+    """The unrounded fp32 product of gate (6144x2048) at batched M against fp64."""
+    (g, _, _), (gh, _, _) = mlp
+    xh = O.gen_normal_bf16(3400, M * H).reshape(M, H)
+    y32 = mq4.quantized_matmul_f32(to_dev_bf16(xh, dev), g.weight, g.scales, g.biases)
+    torch.cuda.synchronize()
+    ref, _ = O.qmm_f64(xh, *gh)
+    err = rel_err_f32(y32.cpu().numpy(), ref)
+    print(f"gate fp32 M={M}: max|err|/rms = {err:.2e}")
+    assert err <= 1e-4

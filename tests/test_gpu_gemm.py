@@ -4,8 +4,10 @@ From M = 33 rows on, mq4_qmm / mq4_qmm_f32 / mq4_qmm_residual /
 mq4_mlp_gate_up_silu run the MFMA GEMM (prefill: the prompt's S tokens through
 qmatmul, src/model/marlin.cpp:18-25, and mlp_forward, :31-35).  Bars, against
 the oracle's fp64 product of the same bf16 inputs and Q4 weights:
-* fp32 output: max|err| <= 1e-2 x rms(ref) (measured ~1e-5: each dequantized
-  weight enters the MFMA as a bf16 hi + lo pair, ~2^-17 relative);
+* fp32 output: max|err| <= 1e-2 x rms(ref), the bar against MLX, and the
+  GEMM's own accuracy bar GEMM_TOL_F32 = 1e-4 x rms (measured ~1e-5), which
+  a single-bf16 weight (~2^-9 relative, ~1e-2 of rms at the maximum over a
+  prefill's outputs) would fail;
 * bf16 output: the fp32 bar plus the output's own rounding, half a bf16 ulp
   of |ref|, and >= 98% bit-identical to bf16(ref);
 * fused SwiGLU: the GEMV's element-wise bar (check_swiglu): >= 99%
@@ -28,6 +30,7 @@ from test_gpu_parity import check_swiglu
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
+GEMM_TOL_F32 = 1e-4
 
 
 def q_host(wq, s, b):
@@ -40,12 +43,12 @@ def make(mq4, O, N, K, sid, dev):
     return (wq, s, b), q_host(wq, s, b)
 
 
-def check_f32(got, ref64, what):
+def check_f32(got, ref64, what, tol=GEMM_TOL_F32):
     ref64 = np.asarray(ref64, np.float64)
     rms = float(np.sqrt(np.mean(ref64 * ref64)))
     err = float(np.max(np.abs(np.asarray(got, np.float64) - ref64))) / rms
     print(f"{what}: fp32 max|err|/rms = {err:.2e}")
-    assert err <= TOL, f"{what}: {err:.3e}"
+    assert err <= min(tol, TOL), f"{what}: {err:.3e}"
 
 
 def check_bf16(O, got_bits, ref64, what):
@@ -130,3 +133,48 @@ def test_gemm_and_gemv_agree_at_the_switch(mq4, O, dev):
     ref64, _ = O.qmm_f64(xh, *qh)
     check_f32(a.cpu().numpy(), ref64[:32], "GEMV M=32")
     check_f32(c.cpu().numpy(), ref64, "GEMM M=33")
+
+
+def sampled_rows(M):
+    return np.unique(np.concatenate([np.arange(0, M, max(1, M // 11)), [M - 1, M - 2, M - 40, 127, 128, 1919, 1920]]))
+
+
+def test_gemm_epilogues_at_prefill_m(mq4, O, dev):
+    """M = 1960 (the 10-frame video turn; its last 128-row tile is ragged):
+    bf16 store, fused SwiGLU, fused (1 + w) RMSNorm + SwiGLU and residual
+    epilogues on sampled rows."""
+    M, N, K = 1960, 6144, 2048
+    print(f"prefill epilogues M={M}", flush=True)
+    rows = sampled_rows(M)
+    (g, gh), (u, uh) = make(mq4, O, N, K, 1000, dev), make(mq4, O, N, K, 1001, dev)
+    G, U = mq4.QuantizedTensor(*g), mq4.QuantizedTensor(*u)
+    x = mq4.fill_normal_bf16((M, K), mq4.STREAM_PREFILL, 0.0, 1.0, device=dev)
+    y = mq4.quantized_matmul(x, *g)
+    y32 = mq4.quantized_matmul_f32(x, *g)
+    h = mq4.mlp_gate_up_silu(x, G, U)
+    nw = mq4.fill_normal_bf16((K,), mq4.stream_id_layer_norm(0), 0.1, 0.02, device=dev)
+    hn = mq4.mlp_gate_up_silu(x, G, U, norm_weight=nw, eps=1e-6)
+    torch.cuda.synchronize()
+    xs = to_host_u16(x)[rows]
+    ref64, _ = O.qmm_f64(xs, *gh)
+    assert np.array_equal(to_host_u16(y), O.f32_to_bf16(y32.cpu().numpy()))
+    check_f32(y32.cpu().numpy()[rows], ref64, "prefill gate fp32")
+    check_bf16(O, to_host_u16(y)[rows], ref64, "prefill gate bf16")
+    _, gb = O.qmm_f64(xs, *gh)
+    _, ub = O.qmm_f64(xs, *uh)
+    check_swiglu(O, to_host_u16(h)[rows], O.swiglu_bf16(gb, ub), "prefill SwiGLU")
+    n = O.rmsnorm_1pw(xs, to_host_u16(nw), 1e-6)
+    _, gbn = O.qmm_f64(n, *gh)
+    _, ubn = O.qmm_f64(n, *uh)
+    check_swiglu(O, to_host_u16(hn)[rows], O.swiglu_bf16(gbn, ubn), "prefill norm+SwiGLU")
+
+    # down projection of h with the residual add (src/model/marlin.cpp:142)
+    (d, dh) = make(mq4, O, K, N, 1002, dev)
+    D = mq4.QuantizedTensor(*d)
+    res = mq4.fill_normal_bf16((M, K), 3001, 0.0, 1.0, device=dev)
+    yr = mq4.qmatmul_residual(h, D, res)
+    yd32 = mq4.quantized_matmul_f32(h, *d)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host_u16(yr), O.add_bf16(to_host_u16(res), O.f32_to_bf16(yd32.cpu().numpy())))
+    ref64d, _ = O.qmm_f64(to_host_u16(h)[rows], *dh)
+    check_f32(yd32.cpu().numpy()[rows], ref64d, "prefill down fp32")

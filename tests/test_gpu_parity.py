@@ -237,7 +237,11 @@ def test_qmm_residual_in_place(mq4, O, dev, M):
     y64, yb = O.qmm_f64(hh, *O.quantize(wh))
     ref = O.add_bf16(rh, yb)
     got = to_host_u16(r)
-    assert O.bf16_ulp_diff(got, ref).max() <= 1
+    # absolute bar: a residual sum that cancels to near zero turns the
+    # product's 1-2 ulp rounding difference into many ulps of the sum
+    err = np.abs(O.bf16_to_f32(got).astype(np.float64) - O.bf16_to_f32(ref))
+    rms = float(np.sqrt(np.mean(y64 * y64)))
+    assert np.all(err <= 2.0 ** -7 * (np.abs(O.bf16_to_f32(yb)) + np.abs(O.bf16_to_f32(ref))) + 2.0 ** -12 * rms)
     assert O.rel_rms_err(got, O.bf16_to_f32(ref).astype(np.float64)) <= TOL
 
 
