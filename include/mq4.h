@@ -164,6 +164,19 @@ int mq4_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K,
                        int64_t N, uint32_t* idx, uint16_t* logits,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* mq4_lm_head_argmax without a workspace: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * per-block partial results live in a static 1 MiB device array inside the
+ * library, one per GPU, held until the process ends; so M <= 32
+ * (MQ4_ERR_UNSUPPORTED above), and calls that overlap in time on one GPU race
+ * (they share that GPU's array).  stream must belong to the current device;
+ * the first call on a device looks the array's address up (no allocation).
+ * Results are identical to mq4_lm_head_argmax's. */
+int mq4_lm_head_argmax_noalloc(const uint16_t* h, int64_t M, int64_t K,
+                               const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                               int64_t N, uint32_t* idx, uint16_t* logits, void* stream);
+
 /* The same with the final (1 + w) RMSNorm fused in front
  * (src/model/marlin.cpp:145, 12-16): logits = bf16(rms_norm(h) @ W^T). */
 int mq4_rmsnorm_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K,

@@ -103,6 +103,7 @@ def lib():
         "mq4_swiglu_bf16": ([P, P, I64, P, P], I),
         "mq4_lm_head_argmax_workspace_size": ([I64, I64], SZ),
         "mq4_lm_head_argmax": ([P, I64, I64, P, P, P, I64, P, P, P, SZ, P], I),
+        "mq4_lm_head_argmax_noalloc": ([P, I64, I64, P, P, P, I64, P, P, P], I),
         "mq4_argmax_workspace_size": ([I64, I64], SZ),
         "mq4_argmax_bf16": ([P, I64, I64, P, P, SZ, P], I),
         "mq4_fill_normal_bf16": ([P, I64, U64, U64, D, D, I64, P], I),

@@ -29,6 +29,8 @@
 //    sums are reduced across the wave by recursive halving, and across the KS
 //    K-split waves of a wave group through LDS.  A block holds NG independent
 //    wave groups.
+#include <mutex>
+
 #include "mq4_device.h"
 #include "mq4_gemm.h"
 #include "mq4_host.h"
@@ -598,9 +600,65 @@ static int lm_head_impl(const char* what, const uint16_t* h, int64_t M, int64_t 
     return launch_status(what);
 }
 
+// ---- lm_head + argmax without a workspace argument ----
+// The per-block partial keys of mq4_lm_head_argmax_noalloc live in this
+// file-scope device array instead of a caller-provided workspace: one copy per
+// GPU the library runs on, held until the process ends, shared by every call
+// on that GPU (so calls that overlap in time on one GPU race).  The partial
+// keys need no initialisation: every launch writes the slots it reads.
+constexpr int kScratchMaxM = 32;
+constexpr size_t kScratchWords = (size_t)kScratchMaxM * kPartialStride;       // 1 MiB
+static __device__ __align__(256) uint64_t scratch[kScratchWords];
+
+// In host code `scratch` names a host-side stand-in, not device memory: the
+// device address of each GPU's copy comes from hipGetSymbolAddress, taken once
+// per device with that device current, and only that address is handed to
+// kernels.
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static uint64_t* g_scratch_dev[kMaxDevices] = {};
+
+static int scratch_for_stream(const char* what, hipStream_t st, uint64_t** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(MQ4_ERR_HIP, "%s: hipGetDevice failed", what);
+    if (st) {
+        hipDevice_t sdev = 0;
+        if (hipStreamGetDevice(st, &sdev) != hipSuccess)
+            return fail(MQ4_ERR_HIP, "%s: hipStreamGetDevice failed", what);
+        if ((int)sdev != dev)
+            return fail(MQ4_ERR_INVALID_ARG, "%s: the stream belongs to device %d, the current device is %d", what,
+                        (int)sdev, dev);
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fail(MQ4_ERR_UNSUPPORTED, "%s: device %d out of range", what, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(MQ4_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed: %s", what, hipGetErrorString(e));
+        g_scratch_dev[dev] = reinterpret_cast<uint64_t*>(ptr);
+    }
+    *out = g_scratch_dev[dev];
+    return MQ4_OK;
+}
+
 }  // namespace mq4
 
 using namespace mq4;
+
+extern "C" int mq4_lm_head_argmax_noalloc(const uint16_t* h, int64_t M, int64_t K, const uint32_t* wq,
+                                          const uint16_t* scales, const uint16_t* biases, int64_t N,
+                                          uint32_t* idx, uint16_t* logits, void* stream) {
+    const char* what = "mq4_lm_head_argmax_noalloc";
+    if (M > kScratchMaxM)
+        return fail(MQ4_ERR_UNSUPPORTED, "%s: M=%lld exceeds the %d rows its static scratch holds", what,
+                    (long long)M, kScratchMaxM);
+    if (M <= 0) return fail(MQ4_ERR_INVALID_ARG, "%s: M=%lld must be positive", what, (long long)M);
+    uint64_t* ws = nullptr;
+    if (int rc = scratch_for_stream(what, as_stream(stream), &ws)) return rc;
+    return lm_head_impl<false>(what, h, M, K, nullptr, 0.0f, wq, scales, biases, N, idx, logits, ws,
+                               kScratchWords * sizeof(uint64_t), stream);
+}
 
 extern "C" int mq4_qmm(const uint16_t* x, int64_t M, int64_t K, const uint32_t* wq,
                        const uint16_t* scales, const uint16_t* biases, int64_t N, int transpose,

@@ -151,3 +151,16 @@ def test_decode_step_validation(mq4):
     assert "layer 1" in last_error(mq4)
     mis = (_Layer * 2)(good, _Layer(*([A16, A16 + 8] + [A16] * 8)))
     assert call(layers=ctypes.cast(mis, ctypes.c_void_p)) == ALIGN
+
+
+def test_noalloc_lm_head_host_validation(mq4):
+    """Rejected on the host, before any HIP call: more rows than the static
+    scratch holds, and non-positive M."""
+    L = mq4.lib()
+    f = L.mq4_lm_head_argmax_noalloc
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64] + [ctypes.c_void_p] * 3 + \
+        [ctypes.c_int64] + [ctypes.c_void_p] * 3
+    assert f(fake(A16), 33, 2048, fake(A16), fake(A16), fake(A16), 1000, fake(A16), None, S) == UNSUPPORTED
+    assert "32" in last_error(mq4)
+    assert f(fake(A16), 0, 2048, fake(A16), fake(A16), fake(A16), 1000, fake(A16), None, S) == INVALID
