@@ -1,0 +1,49 @@
+// Host-side interface shared by the small-M kernel families: the dot2 GEMV
+// (mq4_gemv.hip) and the MFMA batched-decode GEMV (mq4_mfma.hip).  The C
+// entry points of mq4_gemv.hip pick the family from M.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mq4_device.h"
+
+namespace mq4 {
+
+enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3, EPI_STORE_F32 = 4 };
+
+constexpr int kPartialStride = 4096;     // max blocks of an argmax launch
+
+struct GemvParams {
+    const uint16_t* x;       // [m_valid, K]
+    int m_valid;
+    int N, K;
+    QMat A, B;               // B: up projection of the fused gate/up kernel
+    uint16_t* y;             // [m_valid, N] (float for EPI_STORE_F32; may be null for ARGMAX)
+    const uint16_t* res;     // EPI_RESIDUAL: [m_valid, N]
+    const uint16_t* norm_w;  // NORM: [K] (1 + w) RMSNorm weight
+    float eps;
+    uint64_t* partial;       // EPI_ARGMAX: [m_valid, kPartialStride] per-block best keys
+    uint32_t* idx;           // EPI_ARGMAX: [m_valid]
+};
+
+// Rows of x from which the entry points use the MFMA batched-decode GEMV
+// (every weight byte read once for up to kMfmaMaxM rows) instead of the dot2
+// GEMV, which reads the weights once per chunk of 4 rows and is faster up to
+// 4 rows (measured on MI355X at the model's shapes); the MFMA GEMM takes over
+// from kGemmMinM (mq4_gemm.h).
+constexpr int kMfmaMinM = 5;
+constexpr int kMfmaMaxM = 32;
+
+// Enqueue the MFMA GEMV for 1 <= a.m_valid <= kMfmaMaxM; returns 0, or -1 if
+// this K / epilogue combination is not provided (the caller then uses the
+// dot2 GEMV).
+int launch_q4_mfma_gemv(const GemvParams& a, int epi, bool norm, hipStream_t st);
+
+// idx[m] = argmax of the per-block keys partial[m * kPartialStride + 0 .. count).
+void launch_argmax_finalize(const uint64_t* partial, int count, int M, uint32_t* idx, hipStream_t st);
+
+// Compute units of the current device (cached).
+int num_cus();
+
+}  // namespace mq4

@@ -33,31 +33,16 @@
 
 #include "mq4_device.h"
 #include "mq4_gemm.h"
+#include "mq4_gemv.h"
 #include "mq4_host.h"
 
 namespace mq4 {
 
-enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3, EPI_STORE_F32 = 4 };
-
-constexpr int kPartialStride = 4096;     // max blocks of an argmax launch
 // Largest K the entry points accept: 1024 16-byte slices per row, two per
 // lane of eight K-split waves (the M = 1 instance; 4-row chunks of x switch
 // to single rows above K = 16384).  Larger K would need more slices per lane
 // than the register file holds without spilling.
 constexpr int kMaxK = 32768;
-
-struct GemvParams {
-    const uint16_t* x;       // [m_valid, K]
-    int m_valid;
-    int N, K;
-    QMat A, B;               // B: up projection of the fused gate/up kernel
-    uint16_t* y;             // [m_valid, N] (float for EPI_STORE_F32; may be null for ARGMAX)
-    const uint16_t* res;     // EPI_RESIDUAL: [m_valid, N]
-    const uint16_t* norm_w;  // NORM: [K] (1 + w) RMSNorm weight
-    float eps;
-    uint64_t* partial;       // EPI_ARGMAX: [m_valid, kPartialStride] per-block best keys
-    uint32_t* idx;           // EPI_ARGMAX: [m_valid]
-};
 
 template <int SPL, int NMAT, int RPI>
 struct WBatch {
@@ -415,8 +400,13 @@ __global__ __launch_bounds__(256) void rms_norm_1pw_kernel(const uint16_t* __res
 
 constexpr int kRPI = 4;
 
+void launch_argmax_finalize(const uint64_t* partial, int count, int M, uint32_t* idx, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)M), dim3(256), 0, st, partial, count, kPartialStride,
+                       idx);
+}
+
 static int g_cus = 0;
-static int num_cus() {
+int num_cus() {
     if (g_cus == 0) {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -485,25 +475,46 @@ static int dispatch_k(const GemvParams& a, hipStream_t st) {
     return -1;
 }
 
+// The rows m0 .. m0+mc-1 of a call (x, y, residual, argmax partials, indices).
+static GemvParams row_chunk(const GemvParams& base, int m0, int mc, int epi) {
+    GemvParams a = base;
+    a.x = base.x + (int64_t)m0 * base.K;
+    a.m_valid = mc;
+    if (base.y) a.y = base.y + (int64_t)m0 * base.N * (epi == EPI_STORE_F32 ? 2 : 1);
+    if (base.res) a.res = base.res + (int64_t)m0 * base.N;
+    if (base.partial) a.partial = base.partial + (int64_t)m0 * kPartialStride;
+    if (base.idx) a.idx = base.idx + m0;
+    return a;
+}
+
 template <int EPI, bool NORM>
 static int run_gemv(const GemvParams& base, int M, hipStream_t st) {
     // Rows of x are processed in chunks of at most 4 (of 1 when K > 16384,
     // where four rows of activations would not fit the register file).
     const int chunk = (base.K / 32 > 512) ? 1 : 4;
     for (int m0 = 0; m0 < M; m0 += chunk) {
-        GemvParams a = base;
         const int mc = (M - m0) < chunk ? (M - m0) : chunk;
-        a.x = base.x + (int64_t)m0 * base.K;
-        a.m_valid = mc;
-        if (base.y) a.y = base.y + (int64_t)m0 * base.N * (EPI == EPI_STORE_F32 ? 2 : 1);
-        if (base.res) a.res = base.res + (int64_t)m0 * base.N;
-        if (base.partial) a.partial = base.partial + (int64_t)m0 * kPartialStride;
-        if (base.idx) a.idx = base.idx + m0;
+        const GemvParams a = row_chunk(base, m0, mc, EPI);
         int rc;
         if (mc == 1) rc = dispatch_k<1, EPI, NORM>(a, st);
         else if (mc == 2) rc = dispatch_k<2, EPI, NORM>(a, st);
         else rc = dispatch_k<4, EPI, NORM>(a, st);
         if (rc) return rc;
+    }
+    return 0;
+}
+
+// Small-M products: the MFMA GEMV (every weight byte read once per chunk of
+// up to kMfmaMaxM rows) from kMfmaMinM rows on, the dot2 GEMV below that or
+// where the MFMA kernel does not cover K.
+template <int EPI, bool NORM>
+static int run_small(const GemvParams& base, int M, hipStream_t st) {
+    if (M < kMfmaMinM) return run_gemv<EPI, NORM>(base, M, st);
+    for (int m0 = 0; m0 < M; m0 += kMfmaMaxM) {
+        const int mc = (M - m0) < kMfmaMaxM ? (M - m0) : kMfmaMaxM;
+        const GemvParams a = row_chunk(base, m0, mc, EPI);
+        if (launch_q4_mfma_gemv(a, EPI, NORM, st) != 0)
+            if (int rc = run_gemv<EPI, NORM>(a, mc, st)) return rc;
     }
     return 0;
 }
@@ -564,11 +575,11 @@ static int gate_up_impl(const char* what, const uint16_t* x, int64_t M, int64_t 
     GemvParams a = params(x, M, K, N, {gate_wq, gate_scales, gate_biases}, {up_wq, up_scales, up_biases}, h);
     a.norm_w = norm_w;
     a.eps = eps;
-    if (!NORM && M >= kGemmMinM) {   // (the fused RMSNorm variant stays on the GEMV)
+    if (!NORM && M >= kGemmMinM) {   // (the fused RMSNorm variant runs 32-row MFMA GEMV chunks)
         run_gemm(a, M, GEMM_SWIGLU, as_stream(stream));
         return launch_status(what);
     }
-    if (run_gemv<EPI_SWIGLU, NORM>(a, (int)M, as_stream(stream)))
+    if (run_small<EPI_SWIGLU, NORM>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
@@ -595,7 +606,7 @@ static int lm_head_impl(const char* what, const uint16_t* h, int64_t M, int64_t 
     a.eps = eps;
     a.partial = reinterpret_cast<uint64_t*>(workspace);
     a.idx = idx;
-    if (run_gemv<EPI_ARGMAX, NORM>(a, (int)M, as_stream(stream)))
+    if (run_small<EPI_ARGMAX, NORM>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
@@ -674,7 +685,7 @@ extern "C" int mq4_qmm(const uint16_t* x, int64_t M, int64_t K, const uint32_t* 
         run_gemm(a, M, GEMM_STORE, as_stream(stream));
         return launch_status(what);
     }
-    if (run_gemv<EPI_STORE, false>(a, (int)M, as_stream(stream)))
+    if (run_small<EPI_STORE, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
@@ -691,7 +702,7 @@ extern "C" int mq4_qmm_f32(const uint16_t* x, int64_t M, int64_t K, const uint32
         run_gemm(a, M, GEMM_STORE_F32, as_stream(stream));
         return launch_status(what);
     }
-    if (run_gemv<EPI_STORE_F32, false>(a, (int)M, as_stream(stream)))
+    if (run_small<EPI_STORE_F32, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
@@ -709,7 +720,7 @@ extern "C" int mq4_qmm_residual(const uint16_t* x, int64_t M, int64_t K, const u
         run_gemm(a, M, GEMM_RESIDUAL, as_stream(stream));
         return launch_status(what);
     }
-    if (run_gemv<EPI_RESIDUAL, false>(a, (int)M, as_stream(stream)))
+    if (run_small<EPI_RESIDUAL, false>(a, (int)M, as_stream(stream)))
         return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
     return launch_status(what);
 }
