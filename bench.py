@@ -1,24 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark of the MLX-affine Q4 decode path on one MI355X.
+"""Benchmark of the MLX-affine Q4 matrix-product path on one MI355X.
 
-Workload (one "step"): the per-token MLP + lm_head work of marlin-mlx's decode
-loop at M = 1 (src/core/engine.cpp:79-94 -> src/model/marlin.cpp:110-145,
-161-169 -> src/sampling/sampler.cpp:14-16):
+Headline workload (one "step"): the per-token MLP + lm_head work of
+marlin-mlx's decode loop at M = 1 (src/core/engine.cpp:79-94 ->
+src/model/marlin.cpp:110-145, 161-169 -> src/sampling/sampler.cpp:14-16):
     for each of 24 layers:  x = x + down(swiglu(gate n, up n)),  n = rms_norm_l(x)
     token = argmax(lm_head(rms_norm(x)))
 with MLX affine Q4 group-64 weights (gate/up 6144x2048, down 2048x6144, tied
 lm_head 248320x2048), bf16 activations, fp32 accumulation.  rms_norm is the
-reference's (1 + w) RMSNorm (src/model/marlin.cpp:12-16, 141, 145), fused into
-the gate/up and lm_head kernels; without it the 24-layer residual chain grows
-quadratically and overflows bf16.  Weights are
-synthetic N(0, 0.02) bf16 from the counter-based generator, quantized on the
-GPU by this library's pack kernel (timed as well: the quantize/pack of the
-full weight set).  The step is captured once in a HIP graph and replayed.
+reference's (1 + w) RMSNorm (src/model/marlin.cpp:12-16, 141, 145); without it
+the 24-layer residual chain grows quadratically and overflows bf16.  Weights
+are synthetic N(0, 0.02) bf16 from the counter-based generator, quantized on
+the GPU by this library's pack kernel.  The timed path is the one-launch
+decode step (mq4_decode_step), launched back to back; it is checked against
+the 49-kernel chain of the separate entry points (same token and hidden
+state) before timing.
 
 Output: one JSON line on stdout.  `value` is the step's algorithmic HBM
-bandwidth, Q4 weight bytes per step (795,672,576 B) / step time.  Inputs are
-resident in HBM before the timed region; the 796 MB weight stream is larger
+bandwidth, Q4 weight bytes per step (795,672,576 B) / step time; inputs are
+resident in HBM before the timed region and the 796 MB weight stream is larger
 than the 256 MB last-level cache, so every step reads the weights from HBM.
+`configs` holds the other BASELINE configurations, each with its own
+roofline: the single gate GEMV cold and warm (config 1), the 24-layer MLP
+chain (2), lm_head + argmax (3), the prefill GEMM (4), batched decode (5a)
+and the pack of the full weight set (5b).
 """
 from __future__ import annotations
 
@@ -26,15 +31,18 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import statistics
 import sys
 import time
+import traceback
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "Q4 GEMV HBM GB/s (% of 8 TB/s peak); µs per decode-step MLP+lm_head"
 HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0          # MI355X dense bf16 MFMA
 LAYERS, HID, INTER, VOCAB = 24, 2048, 6144, 248320
 EPS = 1e-6
 
@@ -54,12 +62,7 @@ KERNEL_BYTES = {                                  # algorithmic bytes per launch
     # weights + norm weights + x in, token out (activation exchange stays in L2)
     "decode_step": STEP_BYTES + (LAYERS + 1) * 2 * HID + 2 * HID + 4,
 }
-
-
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (separate runs of
-# `bench.py --profile-kernel decode_step`), each scaled by the same counter's reading for a
-# 256 MiB device copy (FETCH x 1.99982, WRITE x 1.0); see profiles/decode_step_m1_hbm_traffic.md.
-MEASURED_TRAFFIC = {"decode_step": 803_470_292 + 6_299_750}
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_step_m1_hbm_traffic.md")
 
 
 def log(*a):
@@ -72,15 +75,30 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--kernel-steps", type=int, default=10,
-                   help="eager steps with per-kernel HIP events (roofline)")
+                   help="eager steps with per-kernel HIP events (separate kernels)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-configs", action="store_true", help="headline only")
     p.add_argument("--cpu-reps", type=int, default=3)
-    p.add_argument("--profile-kernel", choices=["decode_step", "copy"], default=None,
-                   help="counter-collection mode: run only the one-launch decode step (warmup + steps "
-                        "launches) or, to calibrate FETCH_SIZE/WRITE_SIZE, a plain device copy of "
-                        "--copy-mib MiB per launch; prints no JSON line")
+    p.add_argument("--profile-kernel", default=None,
+                   choices=["decode_step", "copy", "gemv_gate", "lm_head", "prefill", "batched", "pack"],
+                   help="counter-collection mode: run only that workload (warmup + steps launches) "
+                        "and print no JSON line; 'copy' calibrates FETCH_SIZE/WRITE_SIZE with a "
+                        "plain device copy of --copy-mib MiB per launch")
     p.add_argument("--copy-mib", type=int, default=256)
+    p.add_argument("--prefill-m", type=int, default=2048)
+    p.add_argument("--batched-m", type=int, default=16)
     return p.parse_args()
+
+
+def measured_traffic():
+    """HBM bytes per decode-step launch from the committed rocprofv3 summary
+    (FETCH_SIZE and WRITE_SIZE runs, calibrated on a device copy)."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9,]+)", text)
+    return int(m.group(1).replace(",", "")) if m else None
 
 
 class Q4:
@@ -94,6 +112,85 @@ class Q4:
                 ctypes.c_void_p(self.b.data_ptr()))
 
 
+class Env:
+    """Library, device, stream helpers and the synthetic model."""
+
+    def __init__(self, torch, mq4, dev):
+        self.torch, self.mq4, self.dev = torch, mq4, dev
+        self.L = mq4.lib()
+        self.P = ctypes.c_void_p
+        self.pack_us = 0.0
+        self.pack_bytes = 0
+        self.ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def st(self):
+        return self.P(self.torch.cuda.current_stream().cuda_stream)
+
+    def make_q4(self, shape, stream_id, timed=True):
+        torch, P, L = self.torch, self.P, self.L
+        N, K = shape
+        w = self.mq4.fill_normal_bf16(shape, stream_id, 0.0, 0.02, device=self.dev)
+        wq = torch.empty((N, K // 8), dtype=torch.int32, device=self.dev)
+        s = torch.empty((N, K // 64), dtype=torch.bfloat16, device=self.dev)
+        b = torch.empty_like(s)
+        e0, e1 = self.ev(), self.ev()
+        e0.record()
+        self.mq4._check(L.mq4_quantize(P(w.data_ptr()), N, K, 64, 4, P(wq.data_ptr()), P(s.data_ptr()),
+                                       P(b.data_ptr()), self.st()))
+        e1.record()
+        torch.cuda.synchronize()
+        if timed:
+            self.pack_us += e0.elapsed_time(e1) * 1e3
+            self.pack_bytes += 2 * N * K + q4_bytes(N, K)
+        del w
+        return Q4(wq, s, b, N, K)
+
+    def timed(self, fn, n, warm=1):
+        """Mean microseconds of fn() launched n times back to back, HIP events on
+        the launch stream around the batch."""
+        for _ in range(warm):
+            fn()
+        self.torch.cuda.synchronize()
+        e0, e1 = self.ev(), self.ev()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        self.torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+
+def hbm_roofline(nbytes, us):
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
+def mfma_roofline(flops, us):
+    tf = flops / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
+def load_oracle():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("mq4_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    O = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(O)
+    return O
+
+
+def host_q4(torch, q):
+    import numpy as np
+    return (q.wq.cpu().numpy().view(np.uint32), q.s.cpu().view(torch.int16).numpy().view(np.uint16),
+            q.b.cpu().view(torch.int16).numpy().view(np.uint16))
+
+
+def host_bf16(torch, t):
+    import numpy as np
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -104,10 +201,10 @@ def main():
     import torch
     import __graft_entry__
     mq4 = __graft_entry__.load_package()
-    L = mq4.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    P = ctypes.c_void_p
+    E = Env(torch, mq4, dev)
+    L, P = E.L, E.P
 
     if args.profile_kernel == "copy":
         n = args.copy_mib * (1 << 20)
@@ -122,49 +219,40 @@ def main():
     # ---------------------------------------------------------------- setup
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; generating + packing "
         f"{LAYERS}x3 MLP matrices and the {VOCAB}x{HID} lm_head")
-    pack_ms = 0.0
-    pack_bytes = 0
-    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
-    def make_q4(shape, stream_id):
-        nonlocal pack_ms, pack_bytes
-        N, K = shape
-        w = mq4.fill_normal_bf16(shape, stream_id, 0.0, 0.02, device=dev)
-        wq = torch.empty((N, K // 8), dtype=torch.int32, device=dev)
-        s = torch.empty((N, K // 64), dtype=torch.bfloat16, device=dev)
-        b = torch.empty_like(s)
-        st = P(torch.cuda.current_stream().cuda_stream)
-        ev_a.record()
-        mq4._check(L.mq4_quantize(P(w.data_ptr()), N, K, 64, 4, P(wq.data_ptr()), P(s.data_ptr()),
-                                  P(b.data_ptr()), st))
-        ev_b.record()
-        torch.cuda.synchronize()
-        pack_ms += ev_a.elapsed_time(ev_b)
-        pack_bytes += 2 * N * K + q4_bytes(N, K)
-        del w
-        return Q4(wq, s, b, N, K)
-
     layers = []
     for l in range(LAYERS):
-        layers.append((make_q4((INTER, HID), mq4.stream_id_layer(l, 0)),
-                       make_q4((INTER, HID), mq4.stream_id_layer(l, 1)),
-                       make_q4((HID, INTER), mq4.stream_id_layer(l, 2))))
-    lm = make_q4((VOCAB, HID), mq4.STREAM_LM_HEAD)
+        layers.append((E.make_q4((INTER, HID), mq4.stream_id_layer(l, 0)),
+                       E.make_q4((INTER, HID), mq4.stream_id_layer(l, 1)),
+                       E.make_q4((HID, INTER), mq4.stream_id_layer(l, 2))))
+    lm = E.make_q4((VOCAB, HID), mq4.STREAM_LM_HEAD)
     norm_w = mq4.fill_normal_bf16((HID,), mq4.STREAM_NORM_WEIGHT, 0.1, 0.02, device=dev)
     layer_norms = [mq4.fill_normal_bf16((HID,), mq4.stream_id_layer_norm(l), 0.1, 0.02, device=dev)
                    for l in range(LAYERS)]
     x0 = mq4.fill_normal_bf16((1, HID), mq4.stream_id_decode_row(0), 0.0, 1.0, device=dev)
     torch.cuda.synchronize()
-    log(f"[bench] pack: {pack_bytes} B in {pack_ms * 1e3:.1f} us "
-        f"({pack_bytes / pack_ms / 1e6:.1f} GB/s)")
+    log(f"[bench] pack: {E.pack_bytes} B in {E.pack_us:.1f} us ({E.pack_bytes / E.pack_us / 1e3:.1f} GB/s)")
 
+    qt = lambda q: mq4.QuantizedTensor(q.wq, q.s, q.b)
+    dec_layers = [mq4.DecoderLayer(layer_norms[l], mq4.MLPWeights(qt(g), qt(u), qt(d)))
+                  for l, (g, u, d) in enumerate(layers)]
+    dstep = mq4.DecodeStep(dec_layers, norm_w, qt(lm), EPS)
+    idx_p = torch.zeros((1,), dtype=torch.int32, device=dev)
+    dargs = lambda st, idx=idx_p, xo=None: (
+        P(x0.data_ptr()), HID, INTER, LAYERS, ctypes.cast(dstep._arr, P), P(norm_w.data_ptr()), EPS,
+        *lm.ptrs(), VOCAB, P(idx.data_ptr()), P(xo.data_ptr()) if xo is not None else None,
+        P(dstep.workspace.data_ptr()), dstep.ws_bytes, st)
+
+    if args.profile_kernel is not None:
+        profile_mode(args, E, layers, lm, norm_w, layer_norms, x0, dstep, dargs)
+        return
+
+    # -------------------------------- separate kernels (the reference chain)
     x = torch.empty((1, HID), dtype=torch.bfloat16, device=dev)
     hbuf = torch.empty((1, INTER), dtype=torch.bfloat16, device=dev)
     idx = torch.zeros((1,), dtype=torch.int32, device=dev)
     ws_bytes = L.mq4_lm_head_argmax_workspace_size(1, VOCAB)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)     # zero once (arrival counters)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
 
-    # Launch list of one step: (kind, callable(stream)).
     def launches():
         out = []
         xp, hp = P(x.data_ptr()), P(hbuf.data_ptr())
@@ -175,8 +263,7 @@ def main():
                         lambda st, xin=xin, nw=nw, g=g, u=u: L.mq4_rmsnorm_gate_up_silu(
                             xin, 1, HID, nw, EPS, *g.ptrs(), *u.ptrs(), INTER, hp, st)))
             out.append(("down_residual",
-                        lambda st, xin=xin, d=d: L.mq4_qmm_residual(
-                            hp, 1, INTER, *d.ptrs(), HID, xin, xp, st)))
+                        lambda st, xin=xin, d=d: L.mq4_qmm_residual(hp, 1, INTER, *d.ptrs(), HID, xin, xp, st)))
         out.append(("norm_lm_head_argmax", lambda st: L.mq4_rmsnorm_lm_head_argmax(
             xp, 1, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB, P(idx.data_ptr()), None,
             P(ws.data_ptr()), ws_bytes, st)))
@@ -184,26 +271,13 @@ def main():
 
     steps = launches()
 
-    if args.profile_kernel == "decode_step":
-        qt = lambda q: mq4.QuantizedTensor(q.wq, q.s, q.b)
-        dec_layers = [mq4.DecoderLayer(layer_norms[l], mq4.MLPWeights(qt(g), qt(u), qt(d)))
-                      for l, (g, u, d) in enumerate(layers)]
-        dstep = mq4.DecodeStep(dec_layers, norm_w, qt(lm), EPS)
-        idx_p = torch.zeros((1,), dtype=torch.int32, device=dev)
-        for _ in range(args.warmup + args.steps):
-            dstep(x0, None, idx_p)
-        torch.cuda.synchronize()
-        log(f"[bench] decode_step: {args.warmup + args.steps} launches, token {int(idx_p.item())}")
-        return
-
     def run_step(st):
         for _, fn in steps:
             rc = fn(st)
             if rc != 0:
                 mq4._check(rc)
 
-    # ------------------------------------------------ eager check + graph
-    run_step(P(torch.cuda.current_stream().cuda_stream))
+    run_step(E.st())
     torch.cuda.synchronize()
     tok_eager = int(idx.item())
     side = torch.cuda.Stream()
@@ -214,93 +288,56 @@ def main():
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        run_step(P(torch.cuda.current_stream().cuda_stream))
+        run_step(E.st())
     torch.cuda.synchronize()
+    us_sep = E.timed(graph.replay, max(args.steps // 4, 5), warm=args.warmup)
+    if int(idx.item()) != tok_eager:
+        raise RuntimeError("separate-kernel graph replay token differs from the eager token")
+    log(f"[bench] separate kernels (HIP graph of 49 launches): {us_sep:.1f} us per step")
 
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    log(f"[bench] warmup done ({args.warmup} graph replays); timing {args.steps} steps")
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    for _ in range(args.steps):
-        graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / args.steps
-    tok_graph = int(idx.item())
-    if tok_graph != tok_eager:
-        raise RuntimeError(f"graph replay token {tok_graph} != eager token {tok_eager}")
-    gbps = STEP_BYTES / (ms_step * 1e-3) / 1e9
-    log(f"[bench] step {ms_step * 1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of "
-        f"8 TB/s), token {tok_graph}")
-
-    # ---------------------------------------- per-kernel HIP-event timing
-    # Each kernel kind is launched back to back (its launches from the step in
-    # order, `--kernel-steps` times over, so weights rotate through all layers
-    # and stay cold) between one pair of HIP events on the stream the kernels
-    # run on; the mean is the batch time over the launch count.  Event pairs
-    # around single launches would add several microseconds of event overhead
-    # per launch.
-    st = P(torch.cuda.current_stream().cuda_stream)
-    nk = args.kernel_steps
+    kernels = {}
+    st = E.st()
     kinds = []
     for kind, _ in steps:
         if kind not in kinds:
             kinds.append(kind)
-    kernels = {}
     for kind in kinds:
         fns = [fn for k, fn in steps if k == kind]
-        for fn in fns:                     # warm the launch path
-            fn(st)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(nk):
-            for fn in fns:
-                fn(st)
-        e1.record()
-        torch.cuda.synchronize()
-        n = nk * len(fns)
-        mean_us = e0.elapsed_time(e1) * 1e3 / n
-        kernels[kind] = {
-            "mean_us": round(mean_us, 3),
-            "launches_per_step": len(fns),
-            "us_per_step": round(mean_us * len(fns), 2),
-            "bytes_per_launch": KERNEL_BYTES[kind],
-            "GBps": round(KERNEL_BYTES[kind] / (mean_us * 1e-6) / 1e9, 1),
-        }
-    dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
-    for k, v in kernels.items():
-        log(f"[bench] kernel {k}: {v}")
-    dk = kernels[dom]
-    roofline = {
-        "kernel": dom,
-        "bound": "hbm",
-        "achieved": dk["GBps"],
-        "peak": HBM_PEAK_GBPS,
-        "unit": "GB/s",
-        "frac": round(dk["GBps"] / HBM_PEAK_GBPS, 4),
-        "traffic": MEASURED_TRAFFIC.get(dom),
-    }
+        nk = args.kernel_steps
+        us = E.timed(lambda: [fn(st) for fn in fns], nk) / len(fns)
+        kernels[kind] = {"mean_us": round(us, 3), "launches_per_step": len(fns),
+                         "us_per_step": round(us * len(fns), 2), "bytes_per_launch": KERNEL_BYTES[kind],
+                         "GBps": round(KERNEL_BYTES[kind] / (us * 1e-6) / 1e9, 1)}
+        log(f"[bench] kernel {kind}: {kernels[kind]}")
 
-    # ------------------------------------ the whole step in one launch
-    # DecodeStep runs the same step as one persistent kernel (same arithmetic,
-    # so the same token and hidden state as the separate kernels above).
-    qt = lambda q: mq4.QuantizedTensor(q.wq, q.s, q.b)
-    dec_layers = [mq4.DecoderLayer(layer_norms[l], mq4.MLPWeights(qt(g), qt(u), qt(d)))
-                  for l, (g, u, d) in enumerate(layers)]
-    dstep = mq4.DecodeStep(dec_layers, norm_w, qt(lm), EPS)
-    idx_p = torch.zeros((1,), dtype=torch.int32, device=dev)
+    # ------------------------------------------------ headline: one launch
     x_p = torch.empty((HID,), dtype=torch.bfloat16, device=dev)
-    run_step(P(torch.cuda.current_stream().cuda_stream))   # x, idx: the separate kernels' result
-    dstep(x0, x_p, idx_p)
+    run_step(E.st())
+    mq4._check(L.mq4_decode_step(*dargs(E.st(), idx_p, x_p)))
     torch.cuda.synchronize()
     tok_p = int(idx_p.item())
     if tok_p != tok_eager or not torch.equal(x_p.view(torch.int16), x.reshape(-1).view(torch.int16)):
         raise RuntimeError(f"one-launch decode step disagrees with the separate kernels "
                            f"(token {tok_p} vs {tok_eager})")
+    log(f"[bench] one-launch step = separate kernels: token {tok_p}, hidden state bit-identical")
+    st = E.st()
+    for _ in range(args.warmup):
+        L.mq4_decode_step(*dargs(st))
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done ({args.warmup} launches); timing {args.steps} steps")
+    t0, t1 = E.ev(), E.ev()
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(args.steps):
+        L.mq4_decode_step(*dargs(st))
+    t1.record()
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / args.steps
+    if int(idx_p.item()) != tok_eager:
+        raise RuntimeError("one-launch decode step: token changed across launches")
+    gbps = STEP_BYTES / (ms_step * 1e-3) / 1e9
+    log(f"[bench] step {ms_step * 1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
+    # the same kernel replayed from a HIP graph (for callers that capture)
     pgraph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -310,64 +347,35 @@ def main():
     torch.cuda.synchronize()
     with torch.cuda.graph(pgraph):
         dstep(x0, None, idx_p)
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        pgraph.replay()
-    torch.cuda.synchronize()
-    t0.record()
-    for _ in range(args.steps):
-        pgraph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    ms_step_p = t0.elapsed_time(t1) / args.steps
-    if int(idx_p.item()) != tok_eager:
-        raise RuntimeError("one-launch decode step: graph replay token differs")
-    log(f"[bench] one-launch step {ms_step_p * 1e3:.1f} us, "
-        f"{STEP_BYTES / (ms_step_p * 1e-3) / 1e9:.0f} GB/s")
-    # kernel duration: back-to-back launches between HIP events on the launch stream
-    st = P(torch.cuda.current_stream().cuda_stream)
-    lay_c = dstep._arr
-    dargs = (P(x0.data_ptr()), HID, INTER, LAYERS, ctypes.cast(lay_c, P), P(norm_w.data_ptr()), EPS,
-             *lm.ptrs(), VOCAB, P(idx_p.data_ptr()), None, P(dstep.workspace.data_ptr()), dstep.ws_bytes, st)
-    mq4._check(L.mq4_decode_step(*dargs))
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n = max(args.kernel_steps * 5, 10)
-    e0.record()
-    for _ in range(n):
-        L.mq4_decode_step(*dargs)
-    e1.record()
-    torch.cuda.synchronize()
-    mean_us = e0.elapsed_time(e1) * 1e3 / n
-    kernels["decode_step"] = {
-        "mean_us": round(mean_us, 3),
-        "launches_per_step": 1,
-        "us_per_step": round(mean_us, 2),
-        "bytes_per_launch": KERNEL_BYTES["decode_step"],
-        "GBps": round(KERNEL_BYTES["decode_step"] / (mean_us * 1e-6) / 1e9, 1),
-    }
-    log(f"[bench] kernel decode_step: {kernels['decode_step']}")
-    sep = {"us_per_step": round(ms_step * 1e3, 2), "GBps": round(gbps, 1),
-           "note": "the same step as 49 separate kernels (24 x [norm+gate/up+SiLU, down+residual], "
-                   "norm+lm_head+argmax, argmax finalize) replayed from one HIP graph"}
-    if ms_step_p < ms_step:
-        ms_step, gbps = ms_step_p, STEP_BYTES / (ms_step_p * 1e-3) / 1e9
-        dom = "decode_step"
-    dk = kernels[dom]
-    roofline = {
-        "kernel": dom,
-        "bound": "hbm",
-        "achieved": dk["GBps"],
-        "peak": HBM_PEAK_GBPS,
-        "unit": "GB/s",
-        "frac": round(dk["GBps"] / HBM_PEAK_GBPS, 4),
-        "traffic": MEASURED_TRAFFIC.get(dom),
-    }
+    us_graph = E.timed(pgraph.replay, max(args.steps // 4, 5), warm=3)
+    kernels["decode_step"] = {"mean_us": round(ms_step * 1e3, 3), "launches_per_step": 1,
+                              "us_per_step": round(ms_step * 1e3, 2),
+                              "bytes_per_launch": KERNEL_BYTES["decode_step"],
+                              "GBps": round(KERNEL_BYTES["decode_step"] / (ms_step * 1e-3) / 1e9, 1),
+                              "graph_replay_us": round(us_graph, 2)}
+    roofline = {"kernel": "decode_step", **hbm_roofline(KERNEL_BYTES["decode_step"], ms_step * 1e3),
+                "traffic": measured_traffic()}
+
+    # ------------------------------------------------------ other configs
+    configs = {}
+    if not args.no_configs:
+        for name, fn in (("config1_gemv_gate", lambda: bench_gemv_gate(E, layers, x0)),
+                         ("config2_mlp_chain", lambda: bench_mlp_chain(E, dec_layers, lm, norm_w, x0)),
+                         ("config3_lm_head_argmax", lambda: bench_lm_head(E, lm, norm_w, x0)),
+                         ("config4_prefill", lambda: bench_prefill(E, layers, args)),
+                         ("config5a_batched", lambda: bench_batched(E, layers, lm, norm_w, layer_norms)),
+                         ("config5b_pack", lambda: bench_pack(E, args))):
+            try:
+                configs[name] = fn()
+                log(f"[bench] {name}: {json.dumps(configs[name])}")
+            except Exception as e:                      # reported, never hidden
+                traceback.print_exc()
+                configs[name] = {"error": f"{type(e).__name__}: {e}"}
 
     # ------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(torch, layers, lm, x0, norm_w, layer_norms, args.cpu_reps, tok_eager)
+        cpu = cpu_baseline(torch, layers, lm, x0, norm_w, layer_norms, args.cpu_reps, tok_eager, configs)
 
     line = {
         "metric": METRIC,
@@ -395,38 +403,225 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
-        "separate_kernels": sep,
-        "path": "one-launch decode step" if dom == "decode_step" else "separate kernels",
-        "pack": {"bytes": pack_bytes, "us": round(pack_ms * 1e3, 1),
-                 "GBps": round(pack_bytes / pack_ms / 1e6, 1),
-                 "frac": round(pack_bytes / pack_ms / 1e6 / HBM_PEAK_GBPS, 4),
-                 "note": "quantize/pack of the full weight set (72 MLP matrices + lm_head), "
-                         "sum of per-matrix HIP-event times"},
-        "token": tok_graph,
+        "separate_kernels": {"us_per_step": round(us_sep, 2),
+                             "GBps": round(STEP_BYTES / (us_sep * 1e-6) / 1e9, 1),
+                             "note": "the same step as 49 separate kernels (24 x [norm+gate/up+SiLU, "
+                                     "down+residual], norm+lm_head+argmax, argmax finalize) replayed "
+                                     "from one HIP graph"},
+        "path": "one-launch decode step (mq4_decode_step), launched back to back",
+        "configs": configs,
+        "token": tok_p,
     }
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(torch, layers, lm, x0, norm_w, layer_norms, reps, tok_gpu):
+# ------------------------------------------------------------------ configs
+
+def bench_gemv_gate(E, layers, x0):
+    """Config 1: one gate GEMV, M=1, 6144x2048 (mq4_qmm).  Cold: rotating over
+    80 distinct gate-shaped matrices (566 MB, more than twice the 256 MB
+    last-level cache); warm: one matrix repeated (it stays in that cache)."""
+    torch, L, P = E.torch, E.L, E.P
+    mats = [g for g, u, d in layers] + [u for g, u, d in layers]
+    extra = [E.make_q4((INTER, HID), 5000 + i, timed=False) for i in range(80 - len(mats))]
+    mats = mats + extra
+    y = torch.empty((1, INTER), dtype=torch.bfloat16, device=E.dev)
+    st = E.st()
+    xp, yp = P(x0.data_ptr()), P(y.data_ptr())
+    nbytes = q4_bytes(INTER, HID) + 2 * HID + 2 * INTER
+    cold = E.timed(lambda: [L.mq4_qmm(xp, 1, HID, *m.ptrs(), INTER, 1, 64, 4, yp, st) for m in mats], 3,
+                   warm=1) / len(mats)
+    m0 = mats[0]
+    warm = E.timed(lambda: L.mq4_qmm(xp, 1, HID, *m0.ptrs(), INTER, 1, 64, 4, yp, st), 200, warm=20)
+    del extra
+    return {"shape": "M=1, N=6144, K=2048 (gate_proj)", "bytes_per_launch": nbytes,
+            "cold_us": round(cold, 3), "warm_us": round(warm, 3),
+            "roofline_cold": hbm_roofline(nbytes, cold), "roofline_warm": hbm_roofline(nbytes, warm),
+            "note": "back-to-back launches between HIP events on the launch stream; cold rotates over "
+                    "80 distinct matrices (566 MB > 2 x 256 MB last-level cache); warm repeats one "
+                    "(served from that cache, so its rate exceeds HBM)"}
+
+
+def bench_mlp_chain(E, dec_layers, lm, norm_w, x0):
+    """Config 2: the 24 SwiGLU MLP layers with the residual chain, M=1 (the
+    one-launch decode step with a 1-row lm_head, so the step is all MLP)."""
+    torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
+    lm1 = mq4.QuantizedTensor(lm.wq[:1].contiguous(), lm.s[:1].contiguous(), lm.b[:1].contiguous())
+    step = mq4.DecodeStep(dec_layers, norm_w, lm1, EPS)
+    idx = torch.zeros((1,), dtype=torch.int32, device=E.dev)
+    st = E.st()
+    a = (P(x0.data_ptr()), HID, INTER, LAYERS, ctypes.cast(step._arr, P), P(norm_w.data_ptr()), EPS,
+         P(lm1.weight.data_ptr()), P(lm1.scales.data_ptr()), P(lm1.biases.data_ptr()), 1, P(idx.data_ptr()),
+         None, P(step.workspace.data_ptr()), step.ws_bytes, st)
+    us = E.timed(lambda: L.mq4_decode_step(*a), 50, warm=5)
+    nbytes = LAYERS * W_MLP
+    return {"shape": "24 x [RMSNorm, gate/up 6144x2048 + SwiGLU, down 2048x6144 + residual], M=1",
+            "weight_bytes": nbytes, "us": round(us, 2), "roofline": hbm_roofline(nbytes, us),
+            "note": "mq4_decode_step with a 1-row lm_head (the final norm and one 1 KB lm_head row "
+                    "are the only extra work)"}
+
+
+def bench_lm_head(E, lm, norm_w, x0):
+    """Config 3: final RMSNorm + lm_head 248320x2048 + greedy argmax, M=1."""
+    torch, L, P = E.torch, E.L, E.P
+    idx = torch.zeros((1,), dtype=torch.int32, device=E.dev)
+    wsb = L.mq4_lm_head_argmax_workspace_size(1, VOCAB)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=E.dev)
+    st = E.st()
+    f = lambda: L.mq4_rmsnorm_lm_head_argmax(P(x0.data_ptr()), 1, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(),
+                                             VOCAB, P(idx.data_ptr()), None, P(ws.data_ptr()), wsb, st)
+    us = E.timed(f, 50, warm=5)
+    nbytes = KERNEL_BYTES["norm_lm_head_argmax"]
+    return {"shape": "M=1, N=248320, K=2048 (+ (1+w) RMSNorm, greedy argmax)", "bytes_per_call": nbytes,
+            "us": round(us, 2), "roofline": hbm_roofline(nbytes, us), "token": int(idx.item()),
+            "note": "two launches per call (GEMV with per-block argmax keys, 4 us finalize); the "
+                    "286 MB weight stream exceeds the last-level cache"}
+
+
+def bench_prefill(E, layers, args):
+    """Config 4: prefill Q4 GEMM (MFMA), M tokens through gate/up + SwiGLU
+    (6144x2048 x2) and down + residual (2048x6144), M in {1960, 2048, 8192}."""
+    torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
+    g, u, d = layers[0]
+    st = E.st()
+    out = {}
+    for M in (1960, 2048, 8192):
+        x = mq4.fill_normal_bf16((M, HID), mq4.STREAM_PREFILL, 0.0, 1.0, device=E.dev)
+        h = torch.empty((M, INTER), dtype=torch.bfloat16, device=E.dev)
+        y = torch.empty((M, HID), dtype=torch.bfloat16, device=E.dev)
+        reps = 3 if M == 8192 else 10
+        us_gu = E.timed(lambda: L.mq4_mlp_gate_up_silu(P(x.data_ptr()), M, HID, *g.ptrs(), *u.ptrs(), INTER,
+                                                       P(h.data_ptr()), st), reps, warm=2)
+        us_dn = E.timed(lambda: L.mq4_qmm_residual(P(h.data_ptr()), M, INTER, *d.ptrs(), HID, P(x.data_ptr()),
+                                                   P(y.data_ptr()), st), reps, warm=2)
+        f_gu, f_dn = 2 * 2.0 * M * INTER * HID, 2.0 * M * HID * INTER
+        out[str(M)] = {"gate_up_silu_us": round(us_gu, 1), "gate_up_silu": mfma_roofline(f_gu, us_gu),
+                       "down_residual_us": round(us_dn, 1), "down_residual": mfma_roofline(f_dn, us_dn),
+                       "mlp_us": round(us_gu + us_dn, 1), "mlp": mfma_roofline(f_gu + f_dn, us_gu + us_dn)}
+        del x, h, y
+    return {"shapes": "M x 2048 @ gate/up 6144x2048 (fused SwiGLU), M x 6144 @ down 2048x6144 (+ residual)",
+            "flops": "2*M*N*K per matrix (algorithmic, bf16 MFMA peak 2.5 PFLOP/s dense)", "M": out}
+
+
+def bench_batched(E, layers, lm, norm_w, layer_norms):
+    """Config 5a: M concurrent token rows through the 24 MLPs (fused norm +
+    gate/up + SwiGLU, down + residual) and norm + lm_head + argmax: one decode
+    step of M streams, the separate entry points replayed from a HIP graph."""
+    torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
+    out = {}
+    for M in (4, 16, 32):
+        x = mq4.fill_normal_bf16((M, HID), 3000, 0.0, 1.0, device=E.dev)
+        xb = torch.empty_like(x)
+        h = torch.empty((M, INTER), dtype=torch.bfloat16, device=E.dev)
+        idx = torch.empty((M,), dtype=torch.int32, device=E.dev)
+        wsb = L.mq4_lm_head_argmax_workspace_size(M, VOCAB)
+        ws = torch.zeros(wsb, dtype=torch.uint8, device=E.dev)
+
+        def step(st):
+            xin = P(x.data_ptr())
+            for l, (g, u, d) in enumerate(layers):
+                mq4._check(L.mq4_rmsnorm_gate_up_silu(xin, M, HID, P(layer_norms[l].data_ptr()), EPS, *g.ptrs(),
+                                                      *u.ptrs(), INTER, P(h.data_ptr()), st))
+                mq4._check(L.mq4_qmm_residual(P(h.data_ptr()), M, INTER, *d.ptrs(), HID, xin, P(xb.data_ptr()), st))
+                xin = P(xb.data_ptr())
+            mq4._check(L.mq4_rmsnorm_lm_head_argmax(xin, M, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB,
+                                                    P(idx.data_ptr()), None, P(ws.data_ptr()), wsb, st))
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step(P(side.cuda_stream))
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g_ = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_):
+            step(E.st())
+        us = E.timed(g_.replay, 10, warm=3)
+        nbytes = STEP_BYTES + M * (LAYERS * (2 * HID * 2 + INTER * 2) + 2 * HID)
+        out[str(M)] = {"us_per_step": round(us, 1), "bytes_per_step": nbytes, "roofline": hbm_roofline(nbytes, us)}
+        del g_
+    return {"workload": "M rows x [24 x (RMSNorm + gate/up 6144x2048 + SwiGLU, down 2048x6144 + residual), "
+                        "RMSNorm + lm_head 248320x2048 + argmax]; MFMA GEMV (M >= 5) / dot2 GEMV (M <= 4)",
+            "M": out}
+
+
+def bench_pack(E, args):
+    """Config 5b: quantize/pack of the full weight set (72 MLP matrices + the
+    lm_head), the per-matrix HIP-event times of the setup summed."""
+    return {"bytes": E.pack_bytes, "us": round(E.pack_us, 1),
+            "roofline": hbm_roofline(E.pack_bytes, E.pack_us),
+            "note": "read 2 B per bf16 weight + write 0.5625 B per weight (words, scales, biases); "
+                    "sum of 73 per-matrix timings"}
+
+
+# ----------------------------------------------------------- profile modes
+
+def profile_mode(args, E, layers, lm, norm_w, layer_norms, x0, dstep, dargs):
+    """Run one workload warmup + steps times for rocprofv3 (no JSON line)."""
+    torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
+    n = args.warmup + args.steps
+    st = E.st()
+    k = args.profile_kernel
+    if k == "decode_step":
+        for _ in range(n):
+            L.mq4_decode_step(*dargs(st))
+    elif k == "gemv_gate":
+        y = torch.empty((1, INTER), dtype=torch.bfloat16, device=E.dev)
+        mats = [g for g, u, d in layers] + [u for g, u, d in layers]
+        for i in range(n):
+            L.mq4_qmm(P(x0.data_ptr()), 1, HID, *mats[i % len(mats)].ptrs(), INTER, 1, 64, 4, P(y.data_ptr()), st)
+    elif k == "lm_head":
+        idx = torch.zeros((1,), dtype=torch.int32, device=E.dev)
+        wsb = L.mq4_lm_head_argmax_workspace_size(1, VOCAB)
+        ws = torch.zeros(wsb, dtype=torch.uint8, device=E.dev)
+        for _ in range(n):
+            L.mq4_rmsnorm_lm_head_argmax(P(x0.data_ptr()), 1, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB,
+                                         P(idx.data_ptr()), None, P(ws.data_ptr()), wsb, st)
+    elif k == "prefill":
+        M = args.prefill_m
+        g, u, d = layers[0]
+        x = mq4.fill_normal_bf16((M, HID), mq4.STREAM_PREFILL, 0.0, 1.0, device=E.dev)
+        h = torch.empty((M, INTER), dtype=torch.bfloat16, device=E.dev)
+        y = torch.empty((M, HID), dtype=torch.bfloat16, device=E.dev)
+        for _ in range(n):
+            L.mq4_mlp_gate_up_silu(P(x.data_ptr()), M, HID, *g.ptrs(), *u.ptrs(), INTER, P(h.data_ptr()), st)
+            L.mq4_qmm_residual(P(h.data_ptr()), M, INTER, *d.ptrs(), HID, P(x.data_ptr()), P(y.data_ptr()), st)
+    elif k == "batched":
+        M = args.batched_m
+        x = mq4.fill_normal_bf16((M, HID), 3000, 0.0, 1.0, device=E.dev)
+        h = torch.empty((M, INTER), dtype=torch.bfloat16, device=E.dev)
+        idx = torch.empty((M,), dtype=torch.int32, device=E.dev)
+        wsb = L.mq4_lm_head_argmax_workspace_size(M, VOCAB)
+        ws = torch.zeros(wsb, dtype=torch.uint8, device=E.dev)
+        for _ in range(n):
+            for l, (g, u, d) in enumerate(layers):
+                L.mq4_rmsnorm_gate_up_silu(P(x.data_ptr()), M, HID, P(layer_norms[l].data_ptr()), EPS, *g.ptrs(),
+                                           *u.ptrs(), INTER, P(h.data_ptr()), st)
+                L.mq4_qmm_residual(P(h.data_ptr()), M, INTER, *d.ptrs(), HID, P(x.data_ptr()), P(x.data_ptr()), st)
+            L.mq4_rmsnorm_lm_head_argmax(P(x.data_ptr()), M, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB,
+                                         P(idx.data_ptr()), None, P(ws.data_ptr()), wsb, st)
+    elif k == "pack":
+        pass                                   # the setup above packed the full weight set once
+    torch.cuda.synchronize()
+    log(f"[bench] profile {k}: {n} iterations")
+
+
+# ------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(torch, layers, lm, x0, norm_w, layer_norms, reps, tok_gpu, configs):
     """The oracle's fp32-accumulating GEMV (OpenMP over rows) running the same
     decode step on the host cores, plus the literal MLX bf16 loop order on one
-    thread over a one-layer sample."""
+    thread over a one-layer sample; also CPU figures for the other configs
+    (bounded samples), filed under each config's cpu_baseline."""
     import numpy as np
-    import importlib.util
-    spec = importlib.util.spec_from_file_location("mq4_oracle", os.path.join(ROOT, "oracle", "oracle.py"))
-    O = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(O)
-
-    def host(q):
-        return (q.wq.cpu().numpy().view(np.uint32), q.s.cpu().view(torch.int16).numpy().view(np.uint16),
-                q.b.cpu().view(torch.int16).numpy().view(np.uint16))
-
+    O = load_oracle()
     log("[bench] cpu baseline: copying Q4 weights to host")
-    hl = [tuple(host(q) for q in lay) for lay in layers]
-    hlm = host(lm)
-    xh = x0.cpu().view(torch.int16).numpy().view(np.uint16).copy()
-    nw = norm_w.cpu().view(torch.int16).numpy().view(np.uint16).copy()
-    lnw = [t.cpu().view(torch.int16).numpy().view(np.uint16).copy() for t in layer_norms]
+    hl = [tuple(host_q4(torch, q) for q in lay) for lay in layers]
+    hlm = host_q4(torch, lm)
+    xh = host_bf16(torch, x0)
+    nw = host_bf16(torch, norm_w)
+    lnw = [host_bf16(torch, t) for t in layer_norms]
+    threads = O.omp_threads()
 
     def step():
         x = xh
@@ -444,7 +639,6 @@ def cpu_baseline(torch, layers, lm, x0, norm_w, layer_norms, reps, tok_gpu):
         tok = step()
         times.append(time.perf_counter() - t)
     sec = statistics.median(times)
-    threads = O.omp_threads()
     # one-thread MLX-order sample: layer 0's three products
     g, u, d = hl[0]
     t = time.perf_counter()
@@ -455,6 +649,63 @@ def cpu_baseline(torch, layers, lm, x0, norm_w, layer_norms, reps, tok_gpu):
     mlx_order_step_s = s1 * STEP_BYTES / W_MLP
     log(f"[bench] cpu fp32/OpenMP step {sec * 1e3:.1f} ms on {threads} threads (token {tok} vs GPU {tok_gpu}); "
         f"MLX-order 1-thread sample {s1 * 1e3:.0f} ms -> {mlx_order_step_s:.2f} s/step")
+
+    def med(fn, r=3):
+        ts = []
+        for _ in range(r):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return statistics.median(ts)
+
+    extra = {}
+    try:
+        # config 1: one gate GEMV
+        s_g = med(lambda: O.qmm_f32(xh, *hl[0][0]), 5)
+        extra["config1_gemv_gate"] = {"value": round(q4_bytes(INTER, HID) / s_g / 1e9, 2), "unit": "GB/s",
+                                      "us": round(s_g * 1e6, 1), "cores": threads, "kind": "port",
+                                      "sample": "the oracle's fp32 GEMV, gate 6144x2048, M=1, median of 5"}
+        # config 2 / 3: the MLP chain and the lm_head alone
+        def mlp_only():
+            x = xh
+            for (g_, u_, d_), w in zip(hl, lnw):
+                n = O.rmsnorm_1pw(x, w, EPS)
+                x = O.add_bf16(x, O.qmm_f32(O.swiglu_bf16(O.qmm_f32(n, *g_), O.qmm_f32(n, *u_)), *d_))
+        s_mlp = med(mlp_only, 3)
+        extra["config2_mlp_chain"] = {"value": round(LAYERS * W_MLP / s_mlp / 1e9, 2), "unit": "GB/s",
+                                      "us": round(s_mlp * 1e6, 1), "cores": threads, "kind": "port",
+                                      "sample": "24 layers of the oracle's chain, median of 3"}
+        s_lm = med(lambda: O.argmax_bf16(O.qmm_f32(O.rmsnorm_1pw(xh, nw, EPS), *hlm)), 3)
+        extra["config3_lm_head_argmax"] = {"value": round(W_LM / s_lm / 1e9, 2), "unit": "GB/s",
+                                           "us": round(s_lm * 1e6, 1), "cores": threads, "kind": "port",
+                                           "sample": "norm + lm_head 248320x2048 + argmax, median of 3"}
+        # config 4: prefill, a 64-row sample of M=2048 scaled
+        xs = O.gen_normal_bf16(4000, 64 * HID).reshape(64, HID)
+        s_p = med(lambda: O.qmm_f32(xs, *hl[0][0]), 2)
+        tf = 2.0 * 64 * INTER * HID / s_p / 1e12
+        extra["config4_prefill"] = {"value": round(tf, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                                    "sample": "the oracle's fp32 product of 64 prefill rows with gate 6144x2048 "
+                                              "(rate per matrix; the GEMM's rate does not depend on M here)"}
+        # config 5a: batched M=16, one layer's MLP scaled to the step
+        x16 = O.gen_normal_bf16(3000, 16 * HID).reshape(16, HID)
+        s_b = med(lambda: O.qmm_f32(O.swiglu_bf16(O.qmm_f32(x16, *hl[0][0]), O.qmm_f32(x16, *hl[0][1])),
+                                    *hl[0][2]), 2)
+        extra["config5a_batched"] = {"value": round(W_MLP / s_b / 1e9, 2), "unit": "GB/s", "cores": threads,
+                                     "kind": "port", "sample": "M=16 through layer 0's MLP (oracle fp32), "
+                                                               "weight bytes / time"}
+        # config 5b: pack, 4 MLP matrices of bf16 weights
+        ws_ = [O.gen_normal_bf16(1000 + i, INTER * HID, 0.0, 0.02).reshape(INTER, HID) for i in range(4)]
+        s_q = med(lambda: [O.quantize(w) for w in ws_], 2)
+        nb = 4 * (2 * INTER * HID + q4_bytes(INTER, HID))
+        extra["config5b_pack"] = {"value": round(nb / s_q / 1e9, 2), "unit": "GB/s", "cores": threads,
+                                  "kind": "port", "sample": "the oracle's quantize of 4 gate-shaped matrices "
+                                                            "(bytes read + written / time)"}
+    except Exception as e:
+        traceback.print_exc()
+        extra["error"] = f"{type(e).__name__}: {e}"
+    for k, v in extra.items():
+        if k in configs and isinstance(configs[k], dict):
+            configs[k]["cpu_baseline"] = v
     return {
         "value": round(STEP_BYTES / sec / 1e9, 2),
         "unit": "GB/s",
