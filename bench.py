@@ -364,7 +364,8 @@ def main():
                          ("config3_lm_head_argmax", lambda: bench_lm_head(E, lm, norm_w, x0)),
                          ("config4_prefill", lambda: bench_prefill(E, layers, args)),
                          ("config5a_batched", lambda: bench_batched(E, layers, lm, norm_w, layer_norms)),
-                         ("config5b_pack", lambda: bench_pack(E, args))):
+                         ("config5b_pack", lambda: bench_pack(E, args)),
+                         ("next_q4_projections", lambda: bench_projections(E, x0))):
             try:
                 configs[name] = fn()
                 log(f"[bench] {name}: {json.dumps(configs[name])}")
@@ -543,6 +544,28 @@ def bench_batched(E, layers, lm, norm_w, layer_norms):
     return {"workload": "M rows x [24 x (RMSNorm + gate/up 6144x2048 + SwiGLU, down 2048x6144 + residual), "
                         "RMSNorm + lm_head 248320x2048 + argmax]; MFMA GEMV (M >= 5) / dot2 GEMV (M <= 4)",
             "M": out}
+
+
+def bench_projections(E, x0):
+    """The model's other projections quantized to Q4 (SSM in_proj_qkv 6144x2048,
+    in_proj_z / out_proj 2048x2048; attention q_proj 4096x2048, k/v_proj
+    512x2048, o_proj 2048x2048), one M=1 GEMV each, rotating over enough
+    distinct copies that the set exceeds the 256 MB last-level cache."""
+    torch, L, P = E.torch, E.L, E.P
+    st = E.st()
+    out = {}
+    for name, (N, K) in (("in_proj_qkv", (6144, 2048)), ("q_proj", (4096, 2048)),
+                         ("o_proj / out_proj / in_proj_z", (2048, 2048)), ("k_proj / v_proj", (512, 2048))):
+        nb = q4_bytes(N, K)
+        copies = max(4, (600 << 20) // nb)
+        mats = [E.make_q4((N, K), 6000 + 97 * i + N, timed=False) for i in range(copies)]
+        y = torch.empty((1, N), dtype=torch.bfloat16, device=E.dev)
+        us = E.timed(lambda: [L.mq4_qmm(P(x0.data_ptr()), 1, K, *m.ptrs(), N, 1, 64, 4, P(y.data_ptr()), st)
+                              for m in mats], 2, warm=1) / len(mats)
+        out[name] = {"N": N, "K": K, "us": round(us, 3), "copies": copies,
+                     "roofline": hbm_roofline(nb + 2 * K + 2 * N, us)}
+        del mats
+    return {"workload": "M=1 GEMV per projection shape, rotating over > 600 MB of distinct copies", "shapes": out}
 
 
 def bench_pack(E, args):

@@ -30,7 +30,7 @@ __all__ = [
     "MQ4Error", "library_path", "lib", "QuantizedTensor", "MLPWeights",
     "quantize", "dequantize", "quantized_matmul", "quantized_matmul_f32", "argmax", "swiglu",
     "quantize_weight", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
-    "lm_head", "lm_head_argmax", "sample_token", "rms_norm", "fill_normal_bf16",
+    "lm_head", "lm_head_argmax", "lm_head_last_row", "sample_token", "rms_norm", "fill_normal_bf16",
     "DecoderLayer", "DecodeStep",
 ]
 
@@ -428,6 +428,21 @@ def lm_head_argmax(hidden: torch.Tensor, w: QuantizedTensor, return_logits: bool
         norm_weight = _need(norm_weight, torch.bfloat16, "norm_weight")
         _check(L.mq4_rmsnorm_lm_head_argmax(_ptr(hidden), M, K, _ptr(norm_weight), eps, *wargs))
     return (idx, logits) if return_logits else idx
+
+
+def lm_head_last_row(hidden: torch.Tensor, w: QuantizedTensor, norm_weight: torch.Tensor | None = None,
+                     eps: float = 1e-6, return_logits: bool = False):
+    """Greedy next token after a prompt: the reference runs the lm_head over
+    all S rows of the prefill hidden state (src/core/engine.cpp:64) and
+    sample_token then keeps the last row (src/sampling/sampler.cpp:10-12);
+    here only that row goes through the (fused norm +) lm_head + argmax.
+    hidden: [S, K] or [1, S, K]; returns the int32 token [1] (and the last
+    row's bf16 logits [1, N] with return_logits)."""
+    fn = "lm_head_last_row"
+    if not isinstance(hidden, torch.Tensor) or hidden.dim() not in (2, 3) or (hidden.dim() == 3 and hidden.shape[0] != 1):
+        raise ValueError(f"{fn}: hidden must be [S, K] or [1, S, K]")
+    last = hidden.reshape(-1, hidden.shape[-1])[-1:]
+    return lm_head_argmax(last.contiguous(), w, return_logits=return_logits, norm_weight=norm_weight, eps=eps)
 
 
 def sample_token(logits: torch.Tensor, temperature: float = 0.0) -> torch.Tensor:

@@ -172,6 +172,17 @@ public:
         return 0;
     }
 
+    // The next token after a prompt: the reference computes the lm_head for
+    // all S rows of the prefill hidden state (src/core/engine.cpp:64) and
+    // sample_token keeps the last row (src/sampling/sampler.cpp:10-12); only
+    // that row's logits matter for a greedy token, so only it is computed.
+    // hidden is the [S, K] (or [1, S, K]) row-major prefill output.
+    Result<int> last_row(const uint16_t* hidden, int64_t S, const uint16_t* final_norm, float eps,
+                         const QuantizedTensor& lm, uint32_t* idx, uint16_t* logits, hipStream_t stream) {
+        if (S <= 0) return Error{MQ4_ERR_INVALID_ARG, "GreedyLmHead::last_row: S must be positive"};
+        return (*this)(hidden + (S - 1) * lm.in_features, 1, final_norm, eps, lm, idx, logits, stream);
+    }
+
 private:
     DeviceBuffer ws_;
     int64_t max_rows_;
