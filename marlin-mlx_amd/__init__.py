@@ -31,7 +31,7 @@ __all__ = [
     "quantize", "dequantize", "quantized_matmul", "quantized_matmul_f32", "argmax", "swiglu",
     "quantize_weight", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
     "lm_head", "lm_head_argmax", "lm_head_last_row", "sample_token", "rms_norm", "fill_normal_bf16",
-    "DecoderLayer", "DecodeStep",
+    "DecoderLayer", "DecodeStep", "save_q4_cache", "load_q4_cache", "quantize_or_load",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -571,3 +571,7 @@ class DecodeStep:
                                      _ptr(idx), _ptr(x_out), _ptr(self.workspace), self.ws_bytes,
                                      _stream(x.device)))
         return idx
+
+
+# on-disk Q4 weight cache (safetensors, MLX naming): see q4cache.py
+from .q4cache import load_q4_cache, quantize_or_load, save_q4_cache  # noqa: E402

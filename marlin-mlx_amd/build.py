@@ -25,6 +25,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmq4.so")
 CPP_DEMO_SRC = os.path.join(ROOT, "tests", "cpp", "mq4_cpp_demo.cpp")
 CPP_DEMO = os.path.join(BUILD, "mq4_cpp_demo")
+CACHE_TOOL_SRC = os.path.join(ROOT, "tests", "cpp", "mq4_cache_tool.cpp")
+CACHE_TOOL = os.path.join(BUILD, "mq4_cache_tool")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -71,6 +73,13 @@ def build(verbose: bool = True) -> str:
         p = subprocess.run(cmd, capture_output=True, text=True)
         if p.returncode != 0:
             raise RuntimeError("C++ demo build failed:\n" + p.stderr)
+    if os.path.exists(CACHE_TOOL_SRC):
+        # host-only C++ check of the safetensors Q4 cache header (tests/cpp)
+        cmd = [HIPCC, "-O2", "-std=c++17", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
+               CACHE_TOOL_SRC, "-o", CACHE_TOOL]
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        if p.returncode != 0:
+            raise RuntimeError("C++ cache tool build failed:\n" + p.stderr)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
     return LIB

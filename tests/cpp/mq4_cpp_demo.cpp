@@ -3,10 +3,13 @@
 // two synthetic layers and an lm_head, run hidden += mlp(rms_norm(hidden))
 // twice, then the greedy lm_head.  Prints the token and the final hidden
 // state's bf16 words so a test can compare them with the Python binding.
+// With a path argument the lm_head also makes a round trip through the
+// on-disk Q4 cache (mq4_cache.hpp) and the greedy head uses the loaded copy.
 #include <cstdio>
 #include <vector>
 
 #include "mq4.hpp"
+#include "mq4_cache.hpp"
 
 #define CHECK(r)                                                                    \
     do {                                                                            \
@@ -21,7 +24,7 @@ static int fill(uint16_t* p, int64_t n, uint64_t sid, double mu, double sigma, h
     return mq4_fill_normal_bf16(p, n, 0x4D41524Cull, sid, mu, sigma, 0, st);
 }
 
-int main() {
+int main(int argc, char** argv) {
     const int64_t H = 512, I = 1024, V = 4096, LAYERS = 2;
     hipStream_t st;
     if (hipStreamCreate(&st) != hipSuccess) return 2;
@@ -43,6 +46,15 @@ int main() {
     if (fill(wtmp.as<uint16_t>(), V * H, 2000, 0.0, 0.02, st)) return 3;
     auto lmq = mq4::quantize_weight(wtmp.as<uint16_t>(), V, H, st);
     CHECK(lmq);
+    if (argc > 1) {   // save the quantized lm_head and continue with the copy loaded back
+        if (hipStreamSynchronize(st) != hipSuccess) return 4;
+        CHECK(mq4::save_q4_cache(argv[1], {{"lm_head", &lmq.value()}}));
+        auto loaded = mq4::load_q4_cache(argv[1]);
+        CHECK(loaded);
+        auto it = loaded.value().find("lm_head");
+        if (it == loaded.value().end()) return 5;
+        lmq.value() = std::move(it->second);
+    }
     mq4::DeviceBuffer final_norm(2 * H), hidden(2 * H), h(2 * I), idx(4);
     if (fill(final_norm.as<uint16_t>(), H, 2001, 0.1, 0.02, st)) return 3;
     if (fill(hidden.as<uint16_t>(), H, 3000, 0.0, 1.0, st)) return 3;
