@@ -365,7 +365,8 @@ def main():
                          ("config4_prefill", lambda: bench_prefill(E, layers, args)),
                          ("config5a_batched", lambda: bench_batched(E, layers, lm, norm_w, layer_norms)),
                          ("config5b_pack", lambda: bench_pack(E, args)),
-                         ("next_q4_projections", lambda: bench_projections(E, x0))):
+                         ("next_q4_projections", lambda: bench_projections(E, x0)),
+                         ("next_sampling", lambda: bench_sampling(E, lm, norm_w, x0))):
             try:
                 configs[name] = fn()
                 log(f"[bench] {name}: {json.dumps(configs[name])}")
@@ -568,6 +569,41 @@ def bench_projections(E, x0):
     return {"workload": "M=1 GEMV per projection shape, rotating over > 600 MB of distinct copies", "shapes": out}
 
 
+_SAMPLING_LOGITS = []            # the logits bench_sampling used, for the CPU baseline
+SAMPLING_CASES = (("temperature 0.7", (0.7, 0, 1.0)), ("temperature 0.7, top_k 50", (0.7, 50, 1.0)),
+                  ("temperature 0.7, top_p 0.9", (0.7, 0, 0.9)),
+                  ("temperature 0.7, top_k 50, top_p 0.9", (0.7, 50, 0.9)))
+
+
+def bench_sampling(E, lm, norm_w, x0):
+    """sample_token after the lm_head (src/sampling/sampler.cpp:18-39) on the
+    248320 logits of one decode row, M=1 (mq4_sample_bf16 with its workspace:
+    the chunked multi-workgroup path).  A short chain of small kernels, so the
+    figure is latency; the bytes that bound it (one read of the logits) are
+    given for scale."""
+    torch, L, P = E.torch, E.L, E.P
+    st = E.st()
+    logits = torch.empty((1, VOCAB), dtype=torch.bfloat16, device=E.dev)
+    idx = torch.zeros((1,), dtype=torch.int32, device=E.dev)
+    wsb = L.mq4_lm_head_argmax_workspace_size(1, VOCAB)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=E.dev)
+    rc = L.mq4_rmsnorm_lm_head_argmax(P(x0.data_ptr()), 1, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB,
+                                      P(idx.data_ptr()), P(logits.data_ptr()), P(ws.data_ptr()), wsb, st)
+    assert rc == 0
+    swb = L.mq4_sample_workspace_size(1, VOCAB)
+    sws = torch.empty(swb, dtype=torch.uint8, device=E.dev)
+    out = {}
+    for name, (t, k, p) in SAMPLING_CASES:
+        def f(t=t, k=k, p=p):
+            L.mq4_sample_bf16(P(logits.data_ptr()), 1, VOCAB, ctypes.c_float(t), k, ctypes.c_float(p), 7,
+                              P(idx.data_ptr()), None, P(sws.data_ptr()), swb, st)
+        out[name] = {"us": round(E.timed(f, 200, warm=10), 2)}
+    _SAMPLING_LOGITS[:] = [logits]
+    return {"workload": "sample_token over 248320 bf16 logits, M=1", "logit_bytes": 2 * VOCAB, "cases": out,
+            "note": "stream-ordered chain: chunk stats, top-k select, top-p mass passes, Gumbel-max "
+                    "draw, final reduce (only the stages a case needs); HIP events around 200 back-to-back calls"}
+
+
 def bench_pack(E, args):
     """Config 5b: quantize/pack of the full weight set (72 MLP matrices + the
     lm_head), the per-matrix HIP-event times of the setup summed."""
@@ -723,6 +759,19 @@ def cpu_baseline(torch, layers, lm, x0, norm_w, layer_norms, reps, tok_gpu, conf
         extra["config5b_pack"] = {"value": round(nb / s_q / 1e9, 2), "unit": "GB/s", "cores": threads,
                                   "kind": "port", "sample": "the oracle's quantize of 4 gate-shaped matrices "
                                                             "(bytes read + written / time)"}
+        # sampling: the oracle's masks (numpy sort-based, as the reference computes them)
+        if "next_sampling" in configs and _SAMPLING_LOGITS:
+            import importlib.util
+            spec = importlib.util.spec_from_file_location("mq4_oracle_sampler",
+                                                          os.path.join(ROOT, "oracle", "sampler.py"))
+            Smp = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(Smp)
+            lg = host_bf16(torch, _SAMPLING_LOGITS[0])
+            s_s = med(lambda: Smp.keep_mask(lg, 0.7, 50, 0.9), 3)
+            extra["next_sampling"] = {"value": round(s_s * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
+                                      "sample": "oracle/sampler.py keep_mask (temperature 0.7, top_k 50, "
+                                                "top_p 0.9) over the same 248320 logits, numpy, median of 3 "
+                                                "(masks only, no draw)"}
     except Exception as e:
         traceback.print_exc()
         extra["error"] = f"{type(e).__name__}: {e}"

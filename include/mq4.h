@@ -40,6 +40,8 @@
  *                        (src/model/marlin.cpp:145)
  *   mq4_argmax_bf16      mx::argmax(last_logits, -1)
  *                        (src/sampling/sampler.cpp:15)
+ *   mq4_sample_bf16      sample_token (src/sampling/sampler.cpp:9-39):
+ *                        temperature, top-k, top-p and the categorical draw
  *   mq4_rms_norm         rms_norm (src/model/marlin.cpp:12-16)
  *   mq4_decode_step      the per-token MLP + lm_head + greedy token loop body
  *                        (src/model/marlin.cpp:110-145, 161-169;
@@ -191,6 +193,38 @@ int mq4_rmsnorm_lm_head_argmax(const uint16_t* h, int64_t M, int64_t K,
  * mq4_argmax_workspace_size. */
 size_t mq4_argmax_workspace_size(int64_t M, int64_t N);
 int mq4_argmax_bf16(const uint16_t* logits, int64_t M, int64_t N, uint32_t* idx,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* sample_token over each row of bf16 logits [M, N] (src/sampling/sampler.cpp:
+ * 9-39), one token per row into idx[m]:
+ *   temperature <= 0: the greedy argmax (lowest index among equal maxima).
+ *   otherwise scaled = float(logit) / temperature, then
+ *     top_k > 0 (and < N): elements below the k-th largest scaled value are
+ *       masked (ties at the k-th value kept; top_k >= N masks nothing);
+ *     0 < top_p < 1: with the kept elements' probabilities sorted ascending
+ *       (equal probabilities in index order), an element is masked when the
+ *       probability mass before it exceeds top_p -- the reference's mask,
+ *       which drops the largest probabilities;
+ *   and the token is drawn from softmax(scaled) over the kept elements by
+ *   Gumbel-max with this library's counter-based generator: a pure function
+ *   of (logits, parameters, seed, m), so equal seeds give equal tokens.  The
+ *   reference draws from MLX's global key instead (its seed field is unused),
+ *   so tokens agree with it in distribution, not draw by draw.
+ * The top-p mass is summed exactly (64-bit fixed point), where the reference
+ * sums in float32; masks agree except where a cumulative sum lies within
+ * float32 rounding of top_p.  NaN logits are never drawn.  keep (may be NULL,
+ * uint8 [M, N]) receives 1 for each element left unmasked (not written when
+ * temperature <= 0).  M <= 65535 and N <= 2^23 (MQ4_ERR_UNSUPPORTED above);
+ * top_k < 0 or a NaN temperature or top_p is MQ4_ERR_INVALID_ARG.
+ * workspace (may be NULL) is device memory of mq4_sample_workspace_size(M, N)
+ * bytes, 256-byte aligned, no initialisation needed: with it, a few long
+ * rows (M <= 128, N >= 8192, N % 8 == 0, 16-byte aligned logits) are split
+ * over many workgroups; without it, or for other shapes (size 0), one
+ * workgroup handles each row.  Both give identical results.  Calls that
+ * overlap in time must use different workspaces. */
+size_t mq4_sample_workspace_size(int64_t M, int64_t N);
+int mq4_sample_bf16(const uint16_t* logits, int64_t M, int64_t N, float temperature, int top_k,
+                    float top_p, uint64_t seed, uint32_t* idx, uint8_t* keep,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------- */

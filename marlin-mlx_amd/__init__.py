@@ -12,7 +12,7 @@ Reference seams mirrored (paths relative to the marlin-mlx repository):
   swiglu                 src/model/marlin.cpp:27-29
   mlp_forward            src/model/marlin.cpp:31-35
   lm_head                src/model/marlin.cpp:161-169
-  sample_token (greedy)  src/sampling/sampler.cpp:9-16
+  sample_token           src/sampling/sampler.cpp:9-39
 and the MLX ops they call: quantize, dequantize, quantized_matmul, argmax.
 
 Tensor conventions: bf16 tensors are torch.bfloat16; packed weights are
@@ -21,6 +21,7 @@ torch.int32 holding the uint32 words of MLX's layout; indices are torch.int32.
 from __future__ import annotations
 
 import ctypes
+import itertools
 import os
 from dataclasses import dataclass
 
@@ -106,6 +107,8 @@ def lib():
         "mq4_lm_head_argmax_noalloc": ([P, I64, I64, P, P, P, I64, P, P, P], I),
         "mq4_argmax_workspace_size": ([I64, I64], SZ),
         "mq4_argmax_bf16": ([P, I64, I64, P, P, SZ, P], I),
+        "mq4_sample_workspace_size": ([I64, I64], SZ),
+        "mq4_sample_bf16": ([P, I64, I64, ctypes.c_float, I, ctypes.c_float, U64, P, P, P, SZ, P], I),
         "mq4_fill_normal_bf16": ([P, I64, U64, U64, D, D, I64, P], I),
         "mq4_rms_norm": ([P, I64, I64, P, ctypes.c_float, P, P], I),
         "mq4_decode_workspace_size": ([I64, I64, I64], SZ),
@@ -445,13 +448,50 @@ def lm_head_last_row(hidden: torch.Tensor, w: QuantizedTensor, norm_weight: torc
     return lm_head_argmax(last.contiguous(), w, return_logits=return_logits, norm_weight=norm_weight, eps=eps)
 
 
-def sample_token(logits: torch.Tensor, temperature: float = 0.0) -> torch.Tensor:
-    """src/sampling/sampler.cpp:9-16: the last row of [1, S, V] logits, greedy.
-    Stochastic sampling (temperature > 0) is outside this library's path."""
-    if temperature > 0.0:
-        raise NotImplementedError("sample_token: only greedy (temperature <= 0) sampling is provided")
-    last = logits[:, -1, :] if logits.dim() == 3 else logits
-    return argmax(last.contiguous(), -1)
+_sample_calls = itertools.count()
+
+
+def sample_token(logits: torch.Tensor, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                 seed: int | None = None, return_keep: bool = False):
+    """sample_token (src/sampling/sampler.cpp:9-39) on the GPU, one kernel.
+
+    logits: bf16 [1, S, V] (the last position is sampled, as the reference
+    slices it) or [M, V] (every row is sampled).  temperature <= 0 is the
+    greedy argmax; otherwise scaled = logits / temperature, top_k > 0 masks
+    everything below the k-th largest value, 0 < top_p < 1 applies the
+    reference's ascending-order mass mask (an element is masked when the
+    probability mass of the smaller elements before it exceeds top_p), and
+    the token is drawn from softmax(scaled) over the unmasked elements.
+    seed: the draw is a pure function of (logits, parameters, seed, row);
+    None takes the next value of a per-process counter, so successive calls
+    draw independently, as the reference's global random key does.
+    Returns int64 [M] (and the uint8 [M, V] keep mask with return_keep,
+    None for the greedy case)."""
+    fn = "sample_token"
+    if not isinstance(logits, torch.Tensor) or logits.dim() not in (2, 3):
+        raise ValueError(f"{fn}: logits must be [1, S, V] or [M, V]")
+    if logits.dim() == 3:
+        if logits.shape[0] != 1:
+            raise ValueError(f"{fn}: [B, S, V] logits need B == 1 (got {tuple(logits.shape)})")
+        logits = logits[0, -1:, :]
+    if int(top_k) < 0:
+        raise ValueError(f"{fn}: top_k must be >= 0")
+    rows = _need(logits, torch.bfloat16, "logits").contiguous()
+    M, V = rows.shape
+    if seed is None:
+        seed = (SEED * 0x9E3779B97F4A7C15 + next(_sample_calls)) & 0xFFFFFFFFFFFFFFFF
+    idx = torch.empty(M, dtype=torch.int32, device=rows.device)
+    keep = None
+    if return_keep and temperature > 0.0:
+        keep = torch.empty((M, V), dtype=torch.uint8, device=rows.device)
+    L = lib()
+    ws_bytes = L.mq4_sample_workspace_size(M, V)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=rows.device) if ws_bytes else None
+    _check(L.mq4_sample_bf16(_ptr(rows), M, V, float(temperature), int(top_k), float(top_p),
+                             int(seed) & 0xFFFFFFFFFFFFFFFF, _ptr(idx), _ptr(keep), _ptr(ws), ws_bytes,
+                             _stream(rows.device)))
+    out = idx.to(torch.int64)
+    return (out, keep) if return_keep else out
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

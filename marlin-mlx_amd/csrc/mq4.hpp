@@ -188,4 +188,45 @@ private:
     int64_t max_rows_;
 };
 
+// The sampling fields of the reference's SamplingConfig
+// (src/core/config.h:60-63); seed drives this library's counter-based
+// generator (the reference's seed field is unused and MLX's global key draws).
+struct SamplingConfig {
+    float temperature = 0.0f;
+    float top_p = 1.0f;
+    int top_k = 0;
+    uint64_t seed = 0;
+};
+
+// sample_token over bf16 logits [M, vocab] (src/sampling/sampler.cpp:9-39),
+// one token per row.  Each call draws with seed + the number of earlier
+// calls, so successive tokens are independent, as the reference's advancing
+// global key makes them; equal (seed, call count) give equal tokens.
+class Sampler {
+public:
+    Sampler(int64_t max_rows, int64_t vocab) : max_rows_(max_rows), vocab_(vocab) {
+        size_t need = 0;
+        for (int64_t m = 1; m <= max_rows; ++m) {
+            const size_t b = mq4_sample_workspace_size(m, vocab);
+            need = b > need ? b : need;
+        }
+        ws_ = DeviceBuffer(need);
+    }
+    Result<int> operator()(const uint16_t* logits, int64_t M, const SamplingConfig& c, uint32_t* idx,
+                           uint8_t* keep, hipStream_t stream) {
+        if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "Sampler: M exceeds max_rows"};
+        const size_t need = mq4_sample_workspace_size(M, vocab_);
+        if (need > ws_.bytes()) return Error{MQ4_ERR_WORKSPACE, "Sampler: workspace allocation failed"};
+        const int rc = mq4_sample_bf16(logits, M, vocab_, c.temperature, c.top_k, c.top_p, c.seed + calls_++, idx,
+                                       keep, need ? ws_.get() : nullptr, need, stream);
+        if (rc != MQ4_OK) return last_error(rc);
+        return 0;
+    }
+
+private:
+    DeviceBuffer ws_;
+    int64_t max_rows_, vocab_;
+    uint64_t calls_ = 0;
+};
+
 }  // namespace mq4

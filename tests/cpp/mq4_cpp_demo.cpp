@@ -55,23 +55,35 @@ int main(int argc, char** argv) {
         if (it == loaded.value().end()) return 5;
         lmq.value() = std::move(it->second);
     }
-    mq4::DeviceBuffer final_norm(2 * H), hidden(2 * H), h(2 * I), idx(4);
+    mq4::DeviceBuffer final_norm(2 * H), hidden(2 * H), h(2 * I), idx(4), logits(2 * V), sidx(8);
     if (fill(final_norm.as<uint16_t>(), H, 2001, 0.1, 0.02, st)) return 3;
     if (fill(hidden.as<uint16_t>(), H, 3000, 0.0, 1.0, st)) return 3;
     for (int l = 0; l < LAYERS; ++l)
         CHECK(mq4::mlp_forward_residual(hidden.as<uint16_t>(), 1, norms[l].as<uint16_t>(), 1e-6f, layers[l],
                                         h.as<uint16_t>(), st));
     mq4::GreedyLmHead head(1, V);
-    CHECK(head(hidden.as<uint16_t>(), 1, final_norm.as<uint16_t>(), 1e-6f, lmq.value(), idx.as<uint32_t>(), nullptr,
-               st));
+    CHECK(head(hidden.as<uint16_t>(), 1, final_norm.as<uint16_t>(), 1e-6f, lmq.value(), idx.as<uint32_t>(),
+               logits.as<uint16_t>(), st));
+    // sample_token on the same logits: temperature 0.8, top-k 50 (seed 5),
+    // then the greedy case (temperature 0), which must give the argmax token
+    mq4::Sampler sampler(1, V);
+    mq4::SamplingConfig cfg;
+    cfg.temperature = 0.8f;
+    cfg.top_k = 50;
+    cfg.seed = 5;
+    CHECK(sampler(logits.as<uint16_t>(), 1, cfg, sidx.as<uint32_t>(), nullptr, st));
+    cfg.temperature = 0.0f;
+    CHECK(sampler(logits.as<uint16_t>(), 1, cfg, sidx.as<uint32_t>() + 1, nullptr, st));
     if (hipStreamSynchronize(st) != hipSuccess) return 4;
+    uint32_t stok[2] = {0, 0};
+    if (hipMemcpy(stok, sidx.get(), 8, hipMemcpyDeviceToHost) != hipSuccess) return 4;
     uint32_t tok = 0;
     std::vector<uint16_t> hid(H);
     if (hipMemcpy(&tok, idx.get(), 4, hipMemcpyDeviceToHost) != hipSuccess) return 4;
     if (hipMemcpy(hid.data(), hidden.get(), 2 * H, hipMemcpyDeviceToHost) != hipSuccess) return 4;
     std::printf("token %u\nhidden", tok);
     for (int64_t i = 0; i < H; ++i) std::printf(" %u", hid[i]);
-    std::printf("\n");
+    std::printf("\nsampled %u greedy %u\n", stok[0], stok[1]);
     (void)hipStreamDestroy(st);
     return 0;
 }

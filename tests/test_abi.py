@@ -105,8 +105,35 @@ def test_python_api_rejects_host_tensors(mq4):
         mq4.quantize(torch.zeros(4, 64, dtype=torch.bfloat16))
     with pytest.raises(TypeError):
         mq4.quantize(torch.zeros(4, 64, dtype=torch.float32))
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):
         mq4.sample_token(torch.zeros(1, 1, 8, dtype=torch.bfloat16), temperature=0.7)
+    with pytest.raises(ValueError):
+        mq4.sample_token(torch.zeros(2, 1, 8, dtype=torch.bfloat16), temperature=0.7)
+    with pytest.raises(ValueError):
+        mq4.sample_token(torch.zeros(1, 8, dtype=torch.bfloat16), temperature=0.7, top_k=-1)
+
+
+def test_sample_validation(mq4):
+    L = mq4.lib()
+    f = ctypes.c_float
+    args = lambda M, N, t, k, p, lg=fake(A16), ix=fake(A16): (lg, M, N, f(t), k, f(p), 7, ix, None, None, 0, S)
+    assert L.mq4_sample_bf16(*args(0, 8, 1.0, 0, 1.0)) == INVALID
+    assert L.mq4_sample_bf16(*args(1, 0, 1.0, 0, 1.0)) == INVALID
+    assert L.mq4_sample_bf16(*args(65536, 8, 1.0, 0, 1.0)) == UNSUPPORTED
+    assert L.mq4_sample_bf16(*args(1, (1 << 23) + 1, 1.0, 0, 1.0)) == UNSUPPORTED
+    assert L.mq4_sample_bf16(*args(1, 8, 1.0, -1, 1.0)) == INVALID
+    assert "top_k" in last_error(mq4)
+    assert L.mq4_sample_bf16(*args(1, 8, float("nan"), 0, 1.0)) == INVALID
+    assert L.mq4_sample_bf16(*args(1, 8, 1.0, 0, float("nan"))) == INVALID
+    assert L.mq4_sample_bf16(*args(1, 8, 1.0, 0, 1.0, lg=None)) == INVALID
+    assert L.mq4_sample_bf16(*args(1, 8, 1.0, 0, 1.0, lg=fake(A16 + 1))) == ALIGN
+    assert L.mq4_sample_bf16(*args(1, 8, 1.0, 0, 1.0, ix=fake(A16 + 2))) == ALIGN
+    # the chunked path needs its whole workspace, 256-byte aligned
+    need = L.mq4_sample_workspace_size(1, 151936)
+    assert need > 0 and L.mq4_sample_workspace_size(1, 1000) == 0 and L.mq4_sample_workspace_size(129, 151936) == 0
+    ws_args = (fake(A16), 1, 151936, f(1.0), 0, f(1.0), 7, fake(A16), None)
+    assert L.mq4_sample_bf16(*ws_args, fake(A16), need - 1, S) == WORKSPACE
+    assert L.mq4_sample_bf16(*ws_args, fake(A16 + 8), need, S) == WORKSPACE
 
 
 class _Layer(ctypes.Structure):

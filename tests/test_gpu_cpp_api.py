@@ -40,3 +40,9 @@ def test_cpp_demo_matches_python_binding(mq4, O, dev):
     assert np.array_equal(to_host_u16(x).reshape(-1), hid)
     assert int(idx.cpu()[0]) == tok
     assert tok == int(O.argmax_bf16(to_host_u16(logits))[0])
+    # mq4::Sampler: the first call draws with seed 5 + 0 calls, the second is greedy
+    words = lines[2].split()
+    assert words[0] == "sampled" and words[2] == "greedy"
+    assert int(words[3]) == tok
+    want = mq4.sample_token(logits, temperature=0.8, top_k=50, seed=5)
+    assert int(words[1]) == int(want.cpu()[0])
