@@ -142,21 +142,12 @@ struct alignas(16) WStageB {
 constexpr int kDmaA = 2 * (RA + 2);  // LDS DMA instructions per gate/up stage
 constexpr int kDmaB = SPL_B + 2;     // per down stage
 
-// Workgroup barrier without a memory fence: waits for this wave's LDS
-// operations only (lgkmcnt), not for outstanding global loads or LDS DMA.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Pin a value in a VGPR at this point of the program: the computation that
 // produces it cannot be moved below (e.g. below a barrier) by the compiler.
 __device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 
-// Wait until at most N vector-memory operations of this wave are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 struct alignas(16) Smem {
     uint32_t xraw[H / 2];          // raw x of the current layer (residual), bf16 pairs

@@ -160,6 +160,17 @@ __device__ __forceinline__ uint32_t argmax_key_index(uint64_t key) {
     return 0xffffffffu - (uint32_t)(key & 0xffffffffu);
 }
 
+// Workgroup barrier without a memory fence: waits for this wave's LDS
+// operations only (lgkmcnt), not for outstanding global loads or LDS DMA.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // ---- cross-lane butterfly on the VALU (no LDS round trip) ----
 // Level OFF pairs lane l with partner(l): OFF = 32 -> l^32 and 16 -> l^16
 // (v_permlane32_swap / v_permlane16_swap, which move two registers at once),

@@ -21,9 +21,12 @@ struct GemmArgs {
     QMat A, B;               // B: up projection of the fused SwiGLU
     void* y;                 // [M, N] bf16 (float for GEMM_STORE_F32)
     const uint16_t* res;     // GEMM_RESIDUAL: [M, N]
+    const uint16_t* norm_w;  // fused (1 + w) RMSNorm of x: [K] bf16, 16-byte aligned
+    float eps;
 };
 
-// Enqueue Y = epilogue(X . W^T) on `st`; 0 or -1 for an unknown epilogue.
-int launch_q4_gemm(const GemmArgs& a, int epi, hipStream_t st);
+// Enqueue Y = epilogue(X . W^T) on `st` (X = rms_norm(x) with norm, for the
+// GEMM_STORE and GEMM_SWIGLU epilogues); 0, or -1 for an unsupported pair.
+int launch_q4_gemm(const GemmArgs& a, int epi, bool norm, hipStream_t st);
 
 }  // namespace mq4

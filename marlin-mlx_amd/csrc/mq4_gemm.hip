@@ -1,34 +1,51 @@
-// Prefill-shaped (large M) MLX-affine Q4 GEMM for gfx950: bf16 MFMA with the
-// weight tiles dequantized into LDS.
+// Prefill-shaped (large M) MLX-affine Q4 GEMM for gfx950: bf16 MFMA on the
+// exact nibbles, the affine scale and offset applied per group in fp32.
 //
 // Replaces mx::quantized_matmul(x, w, s, b, transpose=true, 64, 4) for the
 // prompt-processing call sites: qmatmul (src/model/marlin.cpp:18-25) inside
 // mlp_forward (:31-35) when the hidden state holds all S prompt tokens
 // (src/core/engine.cpp:64, S ~ 2,000 for a 10-frame video turn), with the
-// swiglu (:27-29) and residual (:142) fused into the epilogue.
+// rms_norm in front (:141, :12-16), the swiglu (:27-29) and the residual
+// (:142) fused in.
 //
-//   Y[M, N] = X[M, K] . W[N, K]^T,  W[n, k] = s[n, k/64] * q[n, k] + b[n, k/64]
+//   Y[M, N] = X[M, K] . W[N, K]^T,  W[n, k] = s[n, g] * q[n, k] + b[n, g],  g = k / 64
+//
+// Per group g the MFMA forms D[m, n] = sum_{k in g} x[m, k] * (128 + q[n, k])
+// with both operands exact in bf16 (128 + q is an 8-bit integer, one
+// v_and_or_b32 from two nibbles) and exact products, and the group is folded
+// into the fp32 accumulator as
+//   acc += s * D + (b - 128 s) * X[m, g],   X[m, g] = sum_{k in g} x[m, k],
+// so each weight is used once, untransformed, and the only rounding is the
+// fp32 accumulation (the affine form the GEMV kernels use per 32-element slice).
 //
 // Work decomposition:
-//  * A 256-thread block computes a 128 x 128 tile of Y (two 128 x 128 tiles,
-//    gate and up, for the fused SwiGLU); each wave a 64 x 64 quarter as 2 x 2
-//    v_mfma_f32_32x32x16_bf16 tiles with fp32 accumulators.
-//  * The K loop steps one quantization group (64) at a time.  Per step every
-//    thread loads 16 bytes of packed weights (32 nibbles of one row, one
-//    scale and bias) and 64 bytes of activations, for the next step while the
-//    current one is multiplied (register prefetch, one LDS buffer).
-//  * Staging: each weight is dequantized once per tile in fp32,
-//    w = fma(s, q, b), from the nibble pair (q_p, q_{p+4}) that one
-//    v_and_or_b32 yields as bf16 (128 + q), and split into two bf16 parts,
-//    hi = bf16(w) and lo = bf16(w - hi) (w - hi is exact in fp32): the MFMA
-//    runs x.hi + x.lo, so the products carry ~2^-17 relative error instead of
-//    the 2^-9 of a single bf16 weight (whose accumulated error reaches the
-//    1e-2-of-RMS bound over the millions of outputs of a prefill GEMM).  The
-//    activations are written in the same within-chunk order (x_p, x_{p+4}),
-//    so the MFMA sums the same products over a permuted k: both operands are
-//    read as 8 consecutive LDS bf16 per lane, exactly the MFMA operand layout
-//    (lane l holds row l % 32, k (l / 32) * 8 .. + 7).
+//  * A 256-thread block computes 128 rows x 128 weight columns (one matrix,
+//    128 output columns; or gate and up, 64 output columns each, for the
+//    fused SwiGLU); each wave 64 rows x 64 weight columns as 2 x 2
+//    v_mfma_f32_32x32x16_bf16 tiles, with a per-group accumulator D beside
+//    the running fp32 result.
+//  * Weights go straight from global memory to registers in the MFMA operand
+//    layout: lane l of a tile holds weight row l % 32 and, per group, the four
+//    packed words of its k-half l / 32 (one 16-byte load).  MFMA step ks uses
+//    word ks of each half, so the k-slots of step ks are the 8-element chunks
+//    ks and 4 + ks of the group; the sum over the group is the same.
+//  * Activations go through LDS, double-buffered, one barrier per group: each
+//    thread stages 32 values of one row (register prefetch one group ahead),
+//    writing them in the nibble-pair order (x_p, x_{p+4}) of the weights and
+//    their sum X.  With the fused RMSNorm each staging thread first reads its
+//    half of the row once for the sum of squares (the pair of threads of a
+//    row combine their halves), then stages bf16(x * r * (1 + w)) with the
+//    same per-element formula as the separate norm kernel, so the operand
+//    holds the bf16 values the reference's rms_norm produces.  (Scaling the
+//    result by r after the product instead would move that rounding: about one
+//    bf16 ulp of the pre-activation, which the SwiGLU amplifies at its largest
+//    outputs.)
+//  * XCD-aware block order: when the column blocks divide evenly over the 8
+//    XCDs, each XCD takes a fixed eighth of the column blocks for every row
+//    block, so its weights stay in its own L2 across the row blocks.
 //  * LDS rows are padded to 72 bf16 (144 bytes) against bank conflicts.
+#include <type_traits>
+
 #include "mq4_device.h"
 #include "mq4_gemm.h"
 #include "mq4_host.h"
@@ -37,148 +54,214 @@ namespace mq4 {
 
 namespace gemm {
 
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BM = 128;
 constexpr int kThreads = 256;
-constexpr int LDS_STRIDE = BK + 8;      // bf16 per LDS row
+constexpr int LDS_STRIDE = 72;          // bf16 per LDS row (64 activations + 8 pad)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// 8 bf16 in natural order -> the within-chunk order (v0, v4, v1, v5, v2, v6, v3, v7)
-__device__ __forceinline__ uint4 permute_chunk(const uint4& a) {
-    return make_uint4((a.x & 0xffffu) | (a.z << 16), (a.x >> 16) | (a.z & 0xffff0000u), (a.y & 0xffffu) | (a.w << 16),
-                      (a.y >> 16) | (a.w & 0xffff0000u));
+__device__ __forceinline__ bf16x8_t weight_operand(uint32_t word) {
+    const uint4 q = make_uint4(nib_pair_bf16<0>(word), nib_pair_bf16<1>(word), nib_pair_bf16<2>(word),
+                               nib_pair_bf16<3>(word));
+    return __builtin_bit_cast(bf16x8_t, q);
 }
 
-// One packed word (8 nibbles of a row) -> its 8 dequantized weights in the
-// within-chunk order, pair P = (w_P, w_{P+4}), as bf16 hi and lo parts.
-__device__ __forceinline__ void dequant_word(uint32_t word, float s, float b, uint4& hi, uint4& lo) {
+// weight_operand with the mask (SGPR) and exponent bits (VGPR) held by the
+// caller: one v_and_or_b32 per nibble pair plus a shift for pairs 1-3.
+__device__ __forceinline__ uint32_t nib_pair_k(uint32_t s, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(s), "s"(m), "v"(c));
+    return r;
+}
+__device__ __forceinline__ bf16x8_t weight_operand_k(uint32_t word, uint32_t m, uint32_t c) {
+    const uint4 q = make_uint4(nib_pair_k(word, m, c), nib_pair_k(word >> 4, m, c), nib_pair_k(word >> 8, m, c),
+                               nib_pair_k(word >> 12, m, c));
+    return __builtin_bit_cast(bf16x8_t, q);
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <int EPI, bool NORM>
+__global__ __launch_bounds__(kThreads, 2) void q4_gemm_kernel(GemmArgs p) {
 #pragma clang fp contract(off)
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int P = 0; P < 4; ++P) {
-        const uint32_t pr = P == 0 ? nib_pair_bf16<0>(word)
-                                   : P == 1 ? nib_pair_bf16<1>(word) : P == 2 ? nib_pair_bf16<2>(word) : nib_pair_bf16<3>(word);
-        const float w0 = __builtin_fmaf(s, bf16_to_f32(pr & 0xffffu) - 128.0f, b);   // q exact
-        const float w1 = __builtin_fmaf(s, bf16_to_f32(pr >> 16) - 128.0f, b);
-        h[P] = f32x2_to_bf16x2(w0, w1);
-        l[P] = f32x2_to_bf16x2(w0 - bf16_to_f32(h[P] & 0xffffu), w1 - bf16_to_f32(h[P] >> 16));
-    }
-    hi = make_uint4(h[0], h[1], h[2], h[3]);
-    lo = make_uint4(l[0], l[1], l[2], l[3]);
-}
-
-template <int EPI>
-__global__ __launch_bounds__(kThreads, EPI == GEMM_SWIGLU ? 1 : 2) void q4_gemm_kernel(GemmArgs p) {
     constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
-    __shared__ __align__(16) uint16_t As[BM * LDS_STRIDE];
-    __shared__ __align__(16) uint16_t Bs[NMAT][2][BN * LDS_STRIDE];   // [matrix][hi, lo]
+    constexpr int BN = 128 / NMAT;                      // output columns per block
+    __shared__ __align__(16) uint16_t As[2][BM * LDS_STRIDE];
+    __shared__ __align__(16) float Xs[2][BM];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;           // 2 x 2 waves of 64 x 64
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-    const int M = p.M, N = p.N, K = p.K;
-    const int KT = K / BK, G = K / 64;
+    const int wm = wave >> 1, wn = wave & 1;            // 2 x 2 waves of 64 rows x 64 weight columns
+    const int M = p.M, N = p.N, K = p.K, G = K / 64;
 
-    // staging roles: thread t stages row t/2, half t%2 (32 of the 64 k) of
-    // both the activation tile and the weight tile(s)
+    // block -> (column block, row block)
+    const int NB = (N + BN - 1) / BN, MB = (M + BM - 1) / BM;
+    int nb, mb;
+    {
+        const int b = blockIdx.x;
+        if ((NB & 7) == 0) {
+            const int per = NB >> 3, s = b >> 3;
+            nb = (s % per) * 8 + (b & 7);
+            mb = s / per;
+        } else {
+            nb = b % NB;
+            mb = b / NB;
+        }
+    }
+    const int n0 = nb * BN, m0 = mb * BM;
+    (void)MB;
+
+    // ---- activation staging: thread t holds row t/2, k-half t%2 of each group ----
     const int sr = tid >> 1, sh = tid & 1;
     const int xrow = (m0 + sr) < M ? (m0 + sr) : (M - 1);       // clamped: loads stay in bounds
-    const int wrow = (n0 + sr) < N ? (n0 + sr) : (N - 1);
     const uint4* xsrc = reinterpret_cast<const uint4*>(p.x + (int64_t)xrow * K) + sh * 4;
-    const QMat* mats[2] = {&p.A, &p.B};
+    const uint4* nwsrc = reinterpret_cast<const uint4*>(NORM ? p.norm_w : p.x) + sh * 4;
 
-    uint4 xr[4];
-    uint4 wr[NMAT];
-    uint32_t sv[NMAT], bv[NMAT];
-    auto gload = [&](int kt) {
+    // ---- weight operand: tile j, lane l -> weight row, k-half h = l / 32 ----
+    const int h = lane >> 5, col = lane & 31;
+    const uint4* bsrc[2];
+    const uint16_t* ssrc[2];
+    const uint16_t* bbsrc[2];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) xr[c] = xsrc[kt * (BK / 8) + c];
+    for (int j = 0; j < 2; ++j) {
+        const QMat& Q = (NMAT == 2 && j == 1) ? p.B : p.A;
+        int wrow = NMAT == 2 ? n0 + wn * 32 + col : n0 + wn * 64 + j * 32 + col;
+        wrow = wrow < N ? wrow : N - 1;
+        bsrc[j] = reinterpret_cast<const uint4*>(Q.wq + (int64_t)wrow * (K / 8)) + h;   // + 2g per group
+        ssrc[j] = Q.s + (int64_t)wrow * G;
+        bbsrc[j] = Q.b + (int64_t)wrow * G;
+    }
+
+    uint4 xr[4], nr[4];
+    uint4 wnext[2], wcur[2];
+    uint32_t snext[2], bnext[2], scur[2], bcur[2];
+    auto gload = [&](int g) {
 #pragma unroll
-        for (int t = 0; t < NMAT; ++t) {
-            const QMat& Q = *mats[t];
-            wr[t] = load_nt_u4(reinterpret_cast<const uint4*>(Q.wq + (int64_t)wrow * (K / 8)) + kt * 2 + sh);
-            sv[t] = Q.s[(int64_t)wrow * G + kt];
-            bv[t] = Q.b[(int64_t)wrow * G + kt];
+        for (int c = 0; c < 4; ++c) xr[c] = xsrc[g * 8 + c];
+        if (NORM) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) nr[c] = nwsrc[g * 8 + c];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            wnext[j] = load_nt_u4(bsrc[j] + 2 * g);
+            snext[j] = ssrc[j][g];
+            bnext[j] = bbsrc[j][g];
         }
     };
-    auto stage = [&]() {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            *reinterpret_cast<uint4*>(&As[sr * LDS_STRIDE + sh * 32 + c * 8]) = permute_chunk(xr[c]);
-#pragma unroll
-        for (int t = 0; t < NMAT; ++t) {
-            const float s = bf16_to_f32(sv[t]), b = bf16_to_f32(bv[t]);
-            const uint32_t wd[4] = {wr[t].x, wr[t].y, wr[t].z, wr[t].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint4 hi, lo;
-                dequant_word(wd[j], s, b, hi, lo);
-                *reinterpret_cast<uint4*>(&Bs[t][0][sr * LDS_STRIDE + sh * 32 + j * 8]) = hi;
-                *reinterpret_cast<uint4*>(&Bs[t][1][sr * LDS_STRIDE + sh * 32 + j * 8]) = lo;
-            }
+    float rrow = 0.0f;                                  // 1 / rms of the staged row (fused norm)
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll 4
+        for (int c = 0; c < 4 * G; ++c) {
+            const uint4 v = xsrc[(c >> 2) * 8 + (c & 3)];
+            ss = sumsq_word(ss, v.x);
+            ss = sumsq_word(ss, v.y);
+            ss = sumsq_word(ss, v.z);
+            ss = sumsq_word(ss, v.w);
         }
+        rrow = rms_inv(ss + __shfl_xor(ss, 1), K, p.eps);
+    }
+    auto stage = [&](int buf) {
+        float xsum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            uint4 a = xr[c];
+            if (NORM)
+                a = make_uint4(norm_word(a.x, nr[c].x, rrow), norm_word(a.y, nr[c].y, rrow),
+                               norm_word(a.z, nr[c].z, rrow), norm_word(a.w, nr[c].w, rrow));
+            uint32_t pr[4];
+            xsum = pair_chunk(a, pr, xsum);
+            *reinterpret_cast<uint4*>(&As[buf][sr * LDS_STRIDE + sh * 32 + c * 8]) =
+                make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        }
+        xsum += __shfl_xor(xsum, 1);                    // both halves of the row
+        if (sh == 0) Xs[buf][sr] = xsum;
     };
 
-    f32x16_t acc[NMAT][2][2];
+    f32x16_t acc[2][2];
 #pragma unroll
-    for (int t = 0; t < NMAT; ++t)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[t][i][j][e] = 0.0f;
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    const f32x16_t zero = acc[0][0];
 
     gload(0);
-    stage();
-    __syncthreads();
-    const int arow = wm * 64 + (lane & 31), brow = wn * 64 + (lane & 31), koff = (lane >> 5) * 8;
-    for (int kt = 0; kt < KT; ++kt) {
-        if (kt + 1 < KT) gload(kt + 1);
+    stage(0);
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            bf16x8_t a[2], bm[NMAT][2][2];   // [matrix][hi, lo][column tile]
+    for (int j = 0; j < 2; ++j) {
+        wcur[j] = wnext[j];
+        scur[j] = snext[j];
+        bcur[j] = bnext[j];
+    }
+    __syncthreads();
+    const int arow = wm * 64 + col;
+    for (int g = 0; g < G; ++g) {
+        const int buf = g & 1;
+        if (g + 1 < G) gload(g + 1);
+        f32x16_t D[2][2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8_t a[2], b[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[(arow + i * 32) * LDS_STRIDE + ks * 16 + koff]);
+                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][(arow + i * 32) * LDS_STRIDE + (4 * h + ks) * 8]);
 #pragma unroll
-            for (int t = 0; t < NMAT; ++t)
+            for (int j = 0; j < 2; ++j) b[j] = weight_operand(word_of(wcur[j], ks));
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        bm[t][h][j] =
-                            *reinterpret_cast<const bf16x8_t*>(&Bs[t][h][(brow + j * 32) * LDS_STRIDE + ks * 16 + koff]);
+                for (int j = 0; j < 2; ++j)
+                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], ks == 0 ? zero : D[i][j], 0, 0, 0);
+        }
+        // fold the group: acc += s * D + (b - 128 s) * X
 #pragma unroll
-            for (int t = 0; t < NMAT; ++t)
+        for (int j = 0; j < 2; ++j) {
+            const float s = bf16_to_f32(scur[j]);
+            const float c = affine_c(s, bcur[j]);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 2; ++i) {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        acc[t][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bm[t][0][j], acc[t][i][j], 0, 0, 0);
-                        acc[t][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bm[t][1][j], acc[t][i][j], 0, 0, 0);
+                for (int q = 0; q < 4; ++q) {
+                    const float4 X = *reinterpret_cast<const float4*>(&Xs[buf][wm * 64 + i * 32 + q * 8 + h * 4]);
+                    const float xv[4] = {X.x, X.y, X.z, X.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int e = q * 4 + r;
+                        acc[i][j][e] = __builtin_fmaf(s, D[i][j][e], __builtin_fmaf(c, xv[r], acc[i][j][e]));
                     }
+                }
+            }
         }
-        if (kt + 1 < KT) {
-            __syncthreads();
-            stage();
-            __syncthreads();
+        if (g + 1 < G) {
+            stage(buf ^ 1);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                wcur[j] = wnext[j];
+                scur[j] = snext[j];
+                bcur[j] = bnext[j];
+            }
         }
+        __syncthreads();
     }
 
     // ---- epilogue: lane l of a 32 x 32 tile holds rows (e/4)*8 + (l/32)*4 + e%4, column l%32 ----
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+        for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
+            const int cn = NMAT == 2 ? n0 + wn * 32 + col : n0 + wn * 64 + j * 32 + col;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-                if (row >= M || col >= N) continue;
-                const int64_t o = (int64_t)row * N + col;
-                const float v = acc[0][i][j][e];
+                const int rl = wm * 64 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
+                const int row = m0 + rl;
+                if (row >= M || cn >= N) continue;
+                const int64_t o = (int64_t)row * N + cn;
+                const float v = acc[i][j][e];
                 if (EPI == GEMM_STORE) {
                     reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)f32_to_bf16(v);
                 } else if (EPI == GEMM_STORE_F32) {
@@ -187,27 +270,338 @@ __global__ __launch_bounds__(kThreads, EPI == GEMM_SWIGLU ? 1 : 2) void q4_gemm_
                     reinterpret_cast<uint16_t*>(p.y)[o] =
                         (uint16_t)f32_to_bf16(bf16_to_f32(p.res[o]) + round_bf16(v));
                 } else {
-                    reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)swiglu_bf16(v, acc[NMAT - 1][i][j][e]);
+                    reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)swiglu_bf16(v, acc[i][1][e]);
                 }
             }
         }
 }
 
+// ---------------------------------------------------------------------------
+// The same product with every operand staged by LDS DMA (global_load_lds)
+// through a 3-stage ring, for the epilogues without the fused norm.  A block
+// is WM x WN waves of 64 rows x 64 weight columns each (BM = 64 WM rows,
+// BNW = 64 WN weight columns):
+//  * per group, BM x 64 activations (each row's eight 16-byte chunks
+//    XOR-swizzled by (row / 2) % 8: with 64 LDS banks the 16 lanes of one
+//    ds_read_b128 phase, 16 consecutive rows at one chunk, cover all banks
+//    once), BNW x 32 bytes of packed weights (stored k-half major,
+//    [half][row], so a phase reads 256 contiguous bytes) and the rows' scales
+//    and biases (a 4-byte DMA per row holding groups g & ~1 and g | 1, so the
+//    group count must be even and scales/biases 4-byte aligned; other shapes
+//    take the register-staged kernel above), issued two groups ahead of use
+//    and waited for with an exact vmcnt (nothing else in the loop touches
+//    vector memory);
+//  * the DMA targets of all stages must lie in the first 64 KiB of the
+//    workgroup's LDS (static_assert below);
+//  * barriers carry no memory fence (a fence would wait for the DMA in
+//    flight), and each ring stage is a separate LDS object, so the compiler
+//    sees that reading one stage does not depend on the DMA into another;
+//  * X, the group sums of the activations, come from the MFMA operand
+//    fragments already in registers (each lane holds half a row per group,
+//    v_dot2 with ones, the other half from lane l ^ 32), and the (b - 128 s) X
+//    half of the fold runs on the fp32 MFMA (v_mfma_f32_32x32x2_f32, two
+//    groups per instruction: its A operand is X of the lane's row, its B
+//    operand the lane's column offset), so the VALU fold is acc += s * D only.
+namespace dma {
+
+
+// LDS DMA of 16 (4) bytes per lane from global src to lds + 16 (4) * lane.
+// (Plain functions: inside a kernel template, a direct call of the builtin
+// keeps the host pass from emitting the kernel's launch stub.)
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+}
+
+template <int WM, int WN>
+struct Stage {
+    static constexpr int BM = 64 * WM, BNW = 64 * WN;
+    uint4 a[BM * 8];                      // [row][chunk ^ ((row >> 1) & 7)]
+    uint4 b[2 * BNW];                     // [k-half][weight row]
+    uint32_t sb[2][BNW];                  // scales, biases: groups (g & ~1, g | 1)
+};
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// v_perm_b32 selectors: (lo half of x, lo half of z) and (hi of x, hi of z)
+constexpr uint32_t kPermLo = 0x05040100u, kPermHi = 0x07060302u;
+
+template <int EPI, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN, 1) void q4_gemm_dma_kernel(GemmArgs p) {
+#pragma clang fp contract(off)
+    constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
+    constexpr int NW = WM * WN;
+    constexpr int TBM = 64 * WM, BNW = 64 * WN, BN = BNW / NMAT;
+    constexpr int A_I = TBM * 8 / (64 * NW);            // activation DMA instructions per wave and group
+    constexpr int B_I = 2 * BNW / (64 * NW);            // weight
+    constexpr int SB_I = 2 * BNW / (64 * NW);           // scale/bias
+    constexpr int kDmaPerWave = A_I + B_I + SB_I;
+    static_assert(A_I * 64 * NW == TBM * 8 && B_I * 64 * NW == 2 * BNW, "DMA split");
+    typedef Stage<WM, WN> St;
+    static_assert(S == 2 || S == 3, "ring stages");
+    static_assert((size_t)S * sizeof(St) <= 65536, "LDS DMA targets must lie in the first 64 KiB");
+    typedef typename std::conditional<S == 3, St, char>::type St2;   // no third stage with S = 2
+    __shared__ St st0, st1;
+    __shared__ St2 st2;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int h = lane >> 5, col = lane & 31;
+    const int M = p.M, N = p.N, K = p.K, G = K / 64;
+
+    const int NB = (N + BN - 1) / BN;
+    int nb, mb;
+    {
+        const int b = blockIdx.x;
+        if ((NB & 7) == 0) {
+            const int per = NB >> 3, s = b >> 3;
+            nb = (s % per) * 8 + (b & 7);
+            mb = s / per;
+        } else {
+            nb = b % NB;
+            mb = b / NB;
+        }
+    }
+    const int n0 = nb * BN, m0 = mb * TBM;
+
+    // ---- DMA sources of this lane (group g adds g * 64 elements along K) ----
+    const uint16_t* asrc[A_I];
+#pragma unroll
+    for (int t = 0; t < A_I; ++t) {
+        const int slot = (wave * A_I + t) * 64 + lane;
+        const int r = slot >> 3, c = (slot & 7) ^ ((r >> 1) & 7);
+        const int row = (m0 + r) < M ? (m0 + r) : (M - 1);
+        asrc[t] = p.x + (int64_t)row * K + c * 8;
+    }
+    // weight row r of the block -> matrix and output row
+    auto wrow_of = [&](int r) -> int {
+        const int n = NMAT == 2 ? n0 + (r % (BNW / 2)) : n0 + r;
+        return n < N ? n : N - 1;
+    };
+    auto mat_of = [&](int r) -> const QMat& { return (NMAT == 2 && r >= BNW / 2) ? p.B : p.A; };
+    const uint32_t* bsrc[B_I];
+#pragma unroll
+    for (int t = 0; t < B_I; ++t) {
+        const int q = (wave * B_I + t) * 64 + lane, half = q / BNW, r = q % BNW;
+        bsrc[t] = mat_of(r).wq + (int64_t)wrow_of(r) * (K / 8) + half * 4;
+    }
+    const uint16_t* sbsrc[SB_I];
+#pragma unroll
+    for (int t = 0; t < SB_I; ++t) {
+        const int u = (wave * SB_I + t) * 64 + lane, sel = u / BNW, r = u % BNW;
+        sbsrc[t] = (sel ? mat_of(r).b : mat_of(r).s) + (int64_t)wrow_of(r) * G;
+    }
+    auto issue = [&](int g, St& st) {
+#pragma unroll
+        for (int t = 0; t < A_I; ++t)
+            lds_dma16(asrc[t] + g * 64, &st.a[(wave * A_I + t) * 64]);
+#pragma unroll
+        for (int t = 0; t < B_I; ++t)
+            lds_dma16(bsrc[t] + g * 8, &st.b[(wave * B_I + t) * 64]);
+#pragma unroll
+        for (int t = 0; t < SB_I; ++t)
+            lds_dma4(sbsrc[t] + (g & ~1), &st.sb[0][(wave * SB_I + t) * 64]);
+    };
+
+    // ---- compute roles: weight row of tile j for this lane ----
+    int wr[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wn * 32 + col : wn * 64 + j * 32 + col;
+    const uint32_t ONES = 0x3f803f80u;        // bf16 pair (1, 1)
+    uint32_t nib_mask, nib_exp;               // the nibble-pair constants, set up once
+    asm("s_mov_b32 %0, 0x000f000f" : "=s"(nib_mask));
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(nib_exp));
+
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    const f32x16_t zero = acc[0][0];
+    float xprev[2] = {0.0f, 0.0f}, cprev[2] = {0.0f, 0.0f};
+
+    auto compute = [&](int g, const St& st) {
+        uint4 bw[2];
+        float s[2], c[2];
+        const int sh16 = (g & 1) * 16;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            bw[j] = st.b[h * BNW + wr[j]];
+            s[j] = bf16_to_f32((st.sb[0][wr[j]] >> sh16) & 0xffffu);
+            c[j] = affine_c(s[j], (st.sb[1][wr[j]] >> sh16) & 0xffffu);
+        }
+        f32x16_t D[2][2];
+        float xs[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8_t a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = wm * 64 + i * 32 + col, ch = 4 * h + ks;
+                const uint4 raw = st.a[r * 8 + (ch ^ ((r >> 1) & 7))];
+                xs[i] = dot2_bf16(raw.w, ONES, dot2_bf16(raw.z, ONES, dot2_bf16(raw.y, ONES, dot2_bf16(raw.x, ONES, xs[i]))));
+                // nibble-pair order (x0, x4), (x1, x5), (x2, x6), (x3, x7)
+                const uint4 pr = make_uint4(__builtin_amdgcn_perm(raw.z, raw.x, kPermLo),
+                                            __builtin_amdgcn_perm(raw.z, raw.x, kPermHi),
+                                            __builtin_amdgcn_perm(raw.w, raw.y, kPermLo),
+                                            __builtin_amdgcn_perm(raw.w, raw.y, kPermHi));
+                a[i] = __builtin_bit_cast(bf16x8_t, pr);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = weight_operand_k(word_of(bw[j], ks), nib_mask, nib_exp);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], ks == 0 ? zero : D[i][j], 0, 0, 0);
+        }
+        float X[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) X[i] = xs[i] + __shfl_xor(xs[i], 32);
+        // acc += s * D (VALU) ...
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(s[j], D[i][j][e], acc[i][j][e]);
+        // ... and + (b - 128 s) X on the fp32 MFMA, two groups per instruction:
+        // lanes 0-31 carry the earlier group, lanes 32-63 the later one
+        if ((g & 1) == 0 && g + 1 < G) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) xprev[i] = X[i];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) cprev[j] = c[j];
+        } else {
+            const bool solo = (g & 1) == 0;          // the last group of an odd count
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float xa = h ? (solo ? 0.0f : X[i]) : (solo ? X[i] : xprev[i]);
+                    const float cb = h ? (solo ? 0.0f : c[j]) : (solo ? c[j] : cprev[j]);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, cb, acc[i][j], 0, 0, 0);
+                }
+        }
+    };
+    // Every step issues one group's DMA (past the end: the last group again,
+    // into a stage nobody reads), so exactly kDmaPerWave instructions follow
+    // group g's in each wave when step g waits, and one unconditional vmcnt
+    // serves every step.
+    auto step = [&](int g, const St& cur, St& nxt) {
+        wait_vmcnt<kDmaPerWave * (S - 2)>();
+        lds_barrier();                               // group g is in `cur` for every wave
+        issue(g + S - 1 < G ? g + S - 1 : G - 1, nxt);   // into the stage read in step g - 1
+        compute(g, cur);
+    };
+
+    issue(0, st0);
+    if constexpr (S == 3) issue(G > 1 ? 1 : 0, st1);
+    // whole rounds of S steps without branches inside (a conditional step
+    // would merge DMA states and make the compiler wait for all of them),
+    // then the G % S remaining steps
+    int g0 = 0;
+    if constexpr (S == 3) {
+        for (; g0 + S <= G; g0 += S) {
+            step(g0, st0, st2);
+            step(g0 + 1, st1, st0);
+            step(g0 + 2, st2, st1);
+        }
+        if (g0 < G) step(g0, st0, st2);
+        if (g0 + 1 < G) step(g0 + 1, st1, st0);
+    } else {
+        for (; g0 + S <= G; g0 += S) {
+            step(g0, st0, st1);
+            step(g0 + 1, st1, st0);
+        }
+        if (g0 < G) step(g0, st0, st1);
+    }
+    wait_vmcnt<0>();                                 // no DMA outstanding past the loop
+
+    // ---- epilogue: lane l of a 32 x 32 tile holds rows (e/4)*8 + (l/32)*4 + e%4, column l%32 ----
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
+            const int cn = NMAT == 2 ? n0 + wn * 32 + col : n0 + wn * 64 + j * 32 + col;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
+                if (row >= M || cn >= N) continue;
+                const int64_t o = (int64_t)row * N + cn;
+                const float v = acc[i][j][e];
+                if (EPI == GEMM_STORE) {
+                    reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)f32_to_bf16(v);
+                } else if (EPI == GEMM_STORE_F32) {
+                    reinterpret_cast<float*>(p.y)[o] = v;
+                } else if (EPI == GEMM_RESIDUAL) {
+                    reinterpret_cast<uint16_t*>(p.y)[o] =
+                        (uint16_t)f32_to_bf16(bf16_to_f32(p.res[o]) + round_bf16(v));
+                } else {
+                    reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)swiglu_bf16(v, acc[i][1][e]);
+                }
+            }
+        }
+}
+
+// Blocks of the (WM, WN) layout for an M x N product.
+template <int EPI, int WM, int WN>
+unsigned blocks_of(int M, int N) {
+    constexpr int BN = 64 * WN / (EPI == GEMM_SWIGLU ? 2 : 1);
+    return (unsigned)(((N + BN - 1) / BN) * ((M + 64 * WM - 1) / (64 * WM)));
+}
+
+template <int EPI, int WM, int WN, int S>
+void launch_dma(const GemmArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((q4_gemm_dma_kernel<EPI, WM, WN, S>), dim3(blocks_of<EPI, WM, WN>(a.M, a.N)),
+                       dim3(64 * WM * WN), 0, st, a);
+}
+
+// The layout used for every shape: 2 x 2 waves, 2 stages.  Measured on
+// MI355X at M = 2048 / 8192 against 1 x 2, 1 x 4 and 2 x 2 with 3 stages it
+// is as fast or faster for both the gate/up (N = 6144) and the down
+// (N = 2048) products, with the least LDS (41 KB, so two blocks per CU).
+template <int EPI>
+void launch_dma_auto(const GemmArgs& a, hipStream_t st) {
+    launch_dma<EPI, 2, 2, 2>(a, st);
+}
+
+}  // namespace dma
+
+template <int EPI, bool NORM>
+void launch(const GemmArgs& a, hipStream_t st) {
+    constexpr int BN = EPI == GEMM_SWIGLU ? 64 : 128;
+    const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM));
+    const bool dma_ok = ((a.K / 64) % 2 == 0) && reinterpret_cast<uintptr_t>(a.A.s) % 4 == 0 &&
+                        reinterpret_cast<uintptr_t>(a.A.b) % 4 == 0 &&
+                        (EPI != GEMM_SWIGLU ||
+                         (reinterpret_cast<uintptr_t>(a.B.s) % 4 == 0 && reinterpret_cast<uintptr_t>(a.B.b) % 4 == 0));
+    if (NORM || !dma_ok)
+        hipLaunchKernelGGL((q4_gemm_kernel<EPI, NORM>), dim3(blocks), dim3(kThreads), 0, st, a);
+    else
+        dma::launch_dma_auto<EPI>(a, st);
+}
+
 }  // namespace gemm
 
-int launch_q4_gemm(const GemmArgs& a, int epi, hipStream_t st) {
-    const dim3 grid((unsigned)((a.N + gemm::BN - 1) / gemm::BN), (unsigned)((a.M + gemm::BM - 1) / gemm::BM));
+int launch_q4_gemm(const GemmArgs& a, int epi, bool norm, hipStream_t st) {
+    if (norm) {
+        switch (epi) {
+            case GEMM_STORE: gemm::launch<GEMM_STORE, true>(a, st); break;
+            case GEMM_SWIGLU: gemm::launch<GEMM_SWIGLU, true>(a, st); break;
+            default: return -1;
+        }
+        return 0;
+    }
     switch (epi) {
-        case GEMM_STORE: hipLaunchKernelGGL(gemm::q4_gemm_kernel<GEMM_STORE>, grid, dim3(gemm::kThreads), 0, st, a); break;
-        case GEMM_STORE_F32:
-            hipLaunchKernelGGL(gemm::q4_gemm_kernel<GEMM_STORE_F32>, grid, dim3(gemm::kThreads), 0, st, a);
-            break;
-        case GEMM_RESIDUAL:
-            hipLaunchKernelGGL(gemm::q4_gemm_kernel<GEMM_RESIDUAL>, grid, dim3(gemm::kThreads), 0, st, a);
-            break;
-        case GEMM_SWIGLU:
-            hipLaunchKernelGGL(gemm::q4_gemm_kernel<GEMM_SWIGLU>, grid, dim3(gemm::kThreads), 0, st, a);
-            break;
+        case GEMM_STORE: gemm::launch<GEMM_STORE, false>(a, st); break;
+        case GEMM_STORE_F32: gemm::launch<GEMM_STORE_F32, false>(a, st); break;
+        case GEMM_RESIDUAL: gemm::launch<GEMM_RESIDUAL, false>(a, st); break;
+        case GEMM_SWIGLU: gemm::launch<GEMM_SWIGLU, false>(a, st); break;
         default: return -1;
     }
     return 0;

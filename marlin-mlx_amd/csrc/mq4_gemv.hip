@@ -545,9 +545,9 @@ static int check_norm(const char* what, const uint16_t* norm_w, float eps) {
 
 // From kGemmMinM rows on, the entry points use the MFMA GEMM of mq4_gemm.hip
 // (weights read once per 128-row tile instead of once per 4 rows).
-static int run_gemm(const GemvParams& a, int64_t M, int epi, hipStream_t st) {
-    GemmArgs g{a.x, (int)M, a.N, a.K, a.A, a.B, a.y, a.res};
-    return launch_q4_gemm(g, epi, st);
+static int run_gemm(const GemvParams& a, int64_t M, int epi, hipStream_t st, bool norm = false) {
+    GemmArgs g{a.x, (int)M, a.N, a.K, a.A, a.B, a.y, a.res, a.norm_w, a.eps};
+    return launch_q4_gemm(g, epi, norm, st);
 }
 
 static GemvParams params(const uint16_t* x, int64_t M, int64_t K, int64_t N, QMat A, QMat B, uint16_t* y) {
@@ -575,8 +575,8 @@ static int gate_up_impl(const char* what, const uint16_t* x, int64_t M, int64_t 
     GemvParams a = params(x, M, K, N, {gate_wq, gate_scales, gate_biases}, {up_wq, up_scales, up_biases}, h);
     a.norm_w = norm_w;
     a.eps = eps;
-    if (!NORM && M >= kGemmMinM) {   // (the fused RMSNorm variant runs 32-row MFMA GEMV chunks)
-        run_gemm(a, M, GEMM_SWIGLU, as_stream(stream));
+    if (M >= kGemmMinM) {
+        run_gemm(a, M, GEMM_SWIGLU, as_stream(stream), NORM);
         return launch_status(what);
     }
     if (run_small<EPI_SWIGLU, NORM>(a, (int)M, as_stream(stream)))
