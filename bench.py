@@ -121,6 +121,7 @@ class Env:
         self.P = ctypes.c_void_p
         self.pack_us = 0.0
         self.pack_bytes = 0
+        self.pack_set = []          # (shape, stream id) of every matrix quantized in the setup
         self.ev = lambda: torch.cuda.Event(enable_timing=True)
 
     def st(self):
@@ -142,6 +143,7 @@ class Env:
         if timed:
             self.pack_us += e0.elapsed_time(e1) * 1e3
             self.pack_bytes += 2 * N * K + q4_bytes(N, K)
+            self.pack_set.append((shape, stream_id))
         del w
         return Q4(wq, s, b, N, K)
 
@@ -364,7 +366,7 @@ def main():
                          ("config3_lm_head_argmax", lambda: bench_lm_head(E, lm, norm_w, x0)),
                          ("config4_prefill", lambda: bench_prefill(E, layers, args)),
                          ("config5a_batched", lambda: bench_batched(E, layers, lm, norm_w, layer_norms)),
-                         ("config5b_pack", lambda: bench_pack(E, args)),
+                         ("config5b_pack", lambda: bench_pack(E, layers, lm)),
                          ("next_q4_projections", lambda: bench_projections(E, x0)),
                          ("next_sampling", lambda: bench_sampling(E, lm, norm_w, x0))):
             try:
@@ -604,13 +606,34 @@ def bench_sampling(E, lm, norm_w, x0):
                     "draw, final reduce (only the stages a case needs); HIP events around 200 back-to-back calls"}
 
 
-def bench_pack(E, args):
+def bench_pack(E, layers, lm):
     """Config 5b: quantize/pack of the full weight set (72 MLP matrices + the
-    lm_head), the per-matrix HIP-event times of the setup summed."""
-    return {"bytes": E.pack_bytes, "us": round(E.pack_us, 1),
-            "roofline": hbm_roofline(E.pack_bytes, E.pack_us),
+    lm_head).  The bf16 weights are generated again (the same streams as the
+    setup), then all 73 mq4_quantize calls are launched back to back between
+    one pair of HIP events (median of 3 passes); the packed output must equal
+    the setup's bit for bit.  The setup's per-matrix timings (an event pair and
+    a synchronize around each call, so each includes the launch gap) are
+    reported beside it."""
+    torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
+    srcs = [(mq4.fill_normal_bf16(shape, sid, 0.0, 0.02, device=E.dev), shape) for shape, sid in E.pack_set]
+    outs = [(torch.empty((N, K // 8), dtype=torch.int32, device=E.dev),
+             torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev),
+             torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev)) for _, (N, K) in srcs]
+    st = E.st()
+
+    def pack_all():
+        for (w, (N, K)), (wq, s, b) in zip(srcs, outs):
+            L.mq4_quantize(P(w.data_ptr()), N, K, 64, 4, P(wq.data_ptr()), P(s.data_ptr()), P(b.data_ptr()), st)
+
+    us = statistics.median([E.timed(pack_all, 1, warm=1 if i == 0 else 0) for i in range(3)])
+    ref = [q for lay in layers for q in lay] + [lm]
+    same = all(torch.equal(o[0], r.wq) and torch.equal(o[1], r.s) and torch.equal(o[2], r.b) for o, r in zip(outs, ref))
+    del srcs, outs
+    return {"bytes": E.pack_bytes, "us": round(us, 1), "roofline": hbm_roofline(E.pack_bytes, us),
+            "bit_identical_to_setup": bool(same),
+            "per_matrix_sum_us": round(E.pack_us, 1),
             "note": "read 2 B per bf16 weight + write 0.5625 B per weight (words, scales, biases); "
-                    "sum of 73 per-matrix timings"}
+                    "73 calls back to back between one event pair, median of 3 passes"}
 
 
 # ----------------------------------------------------------- profile modes

@@ -12,9 +12,9 @@
 // row-major [N, K] matrix are consecutive 64-element (128-byte) runs, and the
 // packed words, scales and biases of group g sit at wq[8g..8g+7], scales[g],
 // biases[g].  So the whole matrix is one flat stream of groups and the kernel
-// never needs N or K: each lane reads 16 bytes (8 bf16) and writes one packed
-// word, eight lanes form a group, and a wave covers 8 groups = 1 KiB of input
-// with fully coalesced 16-byte loads and 256-byte word stores.
+// never needs N or K: each lane reads 32 bytes (16 bf16) and writes two packed
+// words per step, four lanes form a group, and a wave covers 16 groups =
+// 2 KiB of input per step with coalesced 16-byte loads and word stores.
 #include "mq4_device.h"
 #include "mq4_host.h"
 
@@ -23,62 +23,112 @@ namespace mq4 {
 __device__ __forceinline__ float mlx_max(float a, float b) { return (a < b) ? b : a; }
 __device__ __forceinline__ float mlx_min(float a, float b) { return (b < a) ? b : a; }
 
+// Code of one element: clamp(rint(x), 0, 15) with NaN -> 0, where x is the
+// quotient (w - bias) / scale.  fmaxf/fminf give the same code as MLX's
+// max/min-then-NaN-check (a NaN quotient lands on 0 either way).
+__device__ __forceinline__ uint32_t code_of(float r) {
+    return (uint32_t)fminf(fmaxf(r, 0.0f), 15.0f);
+}
+
+// The correctly rounded quotient d / scale without a division: inv =
+// RN(1 / scale) is the correctly rounded reciprocal, q0 = RN(d * inv) is
+// within 2 ulps of d / scale, and each correction q' = RN(q + r * inv) with
+// the exact FMA residual r = d - q * scale (Markstein's iteration) leaves it
+// within 1/2 ulp plus a small fraction after the first step and correctly
+// rounded after the second (a quotient of two floats is never a rounding
+// midpoint, so no tie can be decided the wrong way).  This holds without
+// overflow or underflow; an infinite q0 means |d / scale| > 2^127, whose
+// code is the clamp of q0 itself, and an underflowing quotient codes to 0
+// either way (|scale| >= 5e-8: the 1e-7 floor, at most halved by the edge
+// adjustment).  So rint of this quotient equals rint(d / scale) as MLX
+// computes it, element by element.
+__device__ __forceinline__ float quotient(float d, float scale, float inv) {
+#pragma clang fp contract(off)
+    const float q0 = d * inv;
+    if (!(fabsf(q0) <= 3.4028234663852886e38f)) return q0;      // +-inf, or NaN from a NaN d
+    const float r0 = __builtin_fmaf(-q0, scale, d);
+    const float q1 = __builtin_fmaf(r0, inv, q0);
+    const float r1 = __builtin_fmaf(-q1, scale, d);
+    return __builtin_fmaf(r1, inv, q1);
+}
+
+// One group step over 16 values per lane (four lanes form a group).
+__device__ __forceinline__ void pack16(const uint4* v, uint32_t* word, float* scale_out, float* bias_out) {
+#pragma clang fp contract(off)
+    float f[16];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        f[8 * k + 0] = bf16_to_f32(v[k].x & 0xffffu); f[8 * k + 1] = bf16_to_f32(v[k].x >> 16);
+        f[8 * k + 2] = bf16_to_f32(v[k].y & 0xffffu); f[8 * k + 3] = bf16_to_f32(v[k].y >> 16);
+        f[8 * k + 4] = bf16_to_f32(v[k].z & 0xffffu); f[8 * k + 5] = bf16_to_f32(v[k].z >> 16);
+        f[8 * k + 6] = bf16_to_f32(v[k].w & 0xffffu); f[8 * k + 7] = bf16_to_f32(v[k].w >> 16);
+    }
+    // Group extremes; NaN never wins (IEEE maxNum/minNum), matching MLX's
+    // std::max/std::min scan from -inf/+inf.
+    float mx = -__builtin_inff(), mn = __builtin_inff();
+#pragma unroll
+    for (int p = 0; p < 16; ++p) { mx = fmaxf(mx, f[p]); mn = fminf(mn, f[p]); }
+#pragma unroll
+    for (int m = 1; m < 4; m <<= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, m));
+        mn = fminf(mn, __shfl_xor(mn, m));
+    }
+    const float n_bins = 15.0f;
+    const float eps = 1e-7f;
+    float scale = mlx_max((mx - mn) / n_bins, eps);
+    const bool side = fabsf(mn) > fabsf(mx);
+    scale = side ? scale : -scale;
+    const float edge = side ? mn : mx;
+    const float q0 = __builtin_rintf(edge / scale);
+    float bias = 0.0f;
+    if (q0 != 0.0f) {
+        scale = edge / q0;
+        bias = edge;
+    }
+    const float inv = 1.0f / scale;
+    word[0] = word[1] = 0u;
+#pragma unroll
+    for (int p = 0; p < 16; ++p)
+        word[p >> 3] |= code_of(__builtin_rintf(quotient(f[p] - bias, scale, inv))) << (4 * (p & 7));
+    *scale_out = scale;
+    *bias_out = bias;
+}
+
+// Each lane packs two consecutive words (16 weights) per step and takes two
+// steps per loop iteration, with all four 16-byte loads issued first.
 __global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w,
                                                            int64_t n_words,
                                                            uint32_t* __restrict__ wq,
                                                            uint16_t* __restrict__ scales,
                                                            uint16_t* __restrict__ biases) {
-#pragma clang fp contract(off)
+    const int64_t n_pairs = n_words >> 1;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    // The loop bound is block-uniform so the cross-lane reductions below run
-    // with every lane of the wave active.
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < n_words; base += stride) {
-        const int64_t i = base + threadIdx.x;
-        const bool live = i < n_words;   // uniform within each 8-lane group
-        uint4 v = live ? load_nt_u4(w + i) : make_uint4(0u, 0u, 0u, 0u);
-        float f[8];
-        f[0] = bf16_to_f32(v.x & 0xffffu); f[1] = bf16_to_f32(v.x >> 16);
-        f[2] = bf16_to_f32(v.y & 0xffffu); f[3] = bf16_to_f32(v.y >> 16);
-        f[4] = bf16_to_f32(v.z & 0xffffu); f[5] = bf16_to_f32(v.z >> 16);
-        f[6] = bf16_to_f32(v.w & 0xffffu); f[7] = bf16_to_f32(v.w >> 16);
-
-        // Group extremes; NaN never wins (IEEE maxNum/minNum), matching MLX's
-        // std::max/std::min scan from -inf/+inf.
-        float mx = -__builtin_inff(), mn = __builtin_inff();
+    // The loop bound is block-uniform so the cross-lane reductions run with
+    // every lane of the wave active.
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < n_pairs; base += 2 * stride) {
+        int64_t idx[2];
+        bool live[2];
+        uint4 v[2][2];
 #pragma unroll
-        for (int p = 0; p < 8; ++p) { mx = fmaxf(mx, f[p]); mn = fminf(mn, f[p]); }
+        for (int u = 0; u < 2; ++u) {
+            idx[u] = base + u * stride + threadIdx.x;
+            live[u] = idx[u] < n_pairs;          // uniform within each 4-lane group
+            v[u][0] = live[u] ? load_nt_u4(w + 2 * idx[u]) : make_uint4(0u, 0u, 0u, 0u);
+            v[u][1] = live[u] ? load_nt_u4(w + 2 * idx[u] + 1) : make_uint4(0u, 0u, 0u, 0u);
+        }
 #pragma unroll
-        for (int m = 1; m < 8; m <<= 1) {
-            mx = fmaxf(mx, __shfl_xor(mx, m));
-            mn = fminf(mn, __shfl_xor(mn, m));
-        }
-
-        const float n_bins = 15.0f;
-        const float eps = 1e-7f;
-        float scale = mlx_max((mx - mn) / n_bins, eps);
-        const bool side = fabsf(mn) > fabsf(mx);
-        scale = side ? scale : -scale;
-        const float edge = side ? mn : mx;
-        const float q0 = __builtin_rintf(edge / scale);
-        float bias = 0.0f;
-        if (q0 != 0.0f) {
-            scale = edge / q0;
-            bias = edge;
-        }
-
-        uint32_t word = 0;
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            float q = __builtin_rintf((f[p] - bias) / scale);
-            q = mlx_min(mlx_max(q, 0.0f), n_bins);
-            const uint32_t qi = (q == q) ? (uint32_t)q : 0u;   // NaN -> 0
-            word |= qi << (4 * p);
-        }
-        if (live) {
-            wq[i] = word;
-            if ((threadIdx.x & 7) == 0) {
-                scales[i >> 3] = (uint16_t)f32_to_bf16(scale);
-                biases[i >> 3] = (uint16_t)f32_to_bf16(bias);
+        for (int u = 0; u < 2; ++u) {
+            uint32_t word[2];
+            float scale, bias;
+            pack16(v[u], word, &scale, &bias);
+            if (live[u]) {
+                const int64_t i = idx[u];
+                wq[2 * i] = word[0];
+                wq[2 * i + 1] = word[1];
+                if ((threadIdx.x & 3) == 0) {
+                    scales[i >> 2] = (uint16_t)f32_to_bf16(scale);
+                    biases[i >> 2] = (uint16_t)f32_to_bf16(bias);
+                }
             }
         }
     }
@@ -183,9 +233,9 @@ extern "C" int mq4_quantize(const uint16_t* w, int64_t N, int64_t K, int group_s
     if (!aligned(w, 16) || !aligned(wq, 4) || !aligned(scales, 2) || !aligned(biases, 2))
         return fail(MQ4_ERR_ALIGNMENT, "%s: w must be 16-byte aligned, wq 4-byte, scales/biases 2-byte",
                     what);
-    const int64_t n_words = N * (K / 8);
+    const int64_t n_words = N * (K / 8);    // a multiple of 8: whole groups, whole word pairs
     const int block = 256;
-    const int grid = grid_for(n_words, block, 256 * 32);
+    const int grid = grid_for((n_words / 2 + 1) / 2, block, 256 * 32);
     hipLaunchKernelGGL(quantize_g64_kernel, dim3(grid), dim3(block), 0, as_stream(stream),
                        reinterpret_cast<const uint4*>(w), n_words, wq, scales, biases);
     return launch_status(what);

@@ -128,6 +128,40 @@ def test_quantize_planted_ties_and_special_groups(mq4, O, dev):
     assert np.array_equal(to_host_u16(b), rb)
 
 
+def test_quantize_quotients_at_half_integers(mq4, O, dev):
+    """Groups whose values sit on, or one bf16 ulp either side of, the
+    half-integer quotients k + 1/2 of their own scale (where rounding the
+    quotient decides the code), plus denormal-range groups (a reciprocal of
+    the scale overflows) and groups near the bf16 maximum: the kernel's
+    reciprocal-multiply path must give the codes of the exact division."""
+    N, K = 384, 2048
+    rng = np.random.default_rng(11)
+    groups = []
+    for gi in range(N * K // 64):
+        kind = gi % 4
+        if kind <= 1:
+            lo = rng.standard_normal() * 0.02
+            span = abs(rng.standard_normal()) * 0.05 + 1e-3
+            k = rng.integers(0, 15, 64)
+            v = (lo + (k + 0.5) * span / 15).astype(np.float32)
+            v[0], v[1] = lo, lo + span                     # pin the extremes
+            bits = O.f32_to_bf16(v).astype(np.int32)
+            bits[2:] += rng.integers(-1, 2, 62) * (kind == 1)   # one ulp either side
+            groups.append(bits.astype(np.uint16))
+        elif kind == 2:
+            groups.append(O.f32_to_bf16((rng.standard_normal(64) * 1e-39).astype(np.float32)))
+        else:
+            groups.append(O.f32_to_bf16((rng.standard_normal(64) * 1e37).astype(np.float32)))
+    wh = np.stack(groups).reshape(N, K)
+    print(f"quantize half-integer quotients N={N} K={K}", flush=True)
+    wq, s, b = mq4.quantize(to_dev_bf16(wh, dev))
+    torch.cuda.synchronize()
+    rq, rs, rb = O.quantize(wh)
+    assert np.array_equal(to_host_u16(s), rs)
+    assert np.array_equal(to_host_u16(b), rb)
+    assert np.array_equal(words(wq), rq)
+
+
 def test_dequantize_matches_affine_formula(mq4, O, dev):
     N, K = 96, 2048
     w, wh = gen_weight(mq4, O, 9, N, K)
