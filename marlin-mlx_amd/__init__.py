@@ -44,6 +44,7 @@ BITS = 4
 
 # Stream ids of the synthetic-input generator (SplitMix64 seed ^ stream id).
 SEED = 0x4D41524C  # "MARL"
+GEMM_MIN_M = 33     # rows from which the C entry points take the MFMA GEMM (mq4_gemm.h kGemmMinM)
 
 
 def stream_id_layer(layer: int, proj: int) -> int:
@@ -342,7 +343,11 @@ def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor
                      norm_weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
     """swiglu(qmatmul(x, gate), qmatmul(x, up)) in one pass over both weights;
     with norm_weight, x is first rms_norm'ed with the (1 + w) multiplier
-    (src/model/marlin.cpp:141) inside the same kernel."""
+    (src/model/marlin.cpp:141): inside the same kernel for decode-sized M,
+    and as the separate norm kernel into a temporary followed by the GEMM from
+    33 rows on (the prefill GEMM with the norm fused re-reads each row block
+    for its norm statistics; the two launches are faster and give the same
+    normalized operand)."""
     fn = "mlp_gate_up_silu"
     _require_quantized(gate, fn)
     _require_quantized(up, fn)
@@ -358,6 +363,9 @@ def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor
     u = (_ptr(up.weight), _ptr(up.scales), _ptr(up.biases))
     if norm_weight is None:
         _check(lib().mq4_mlp_gate_up_silu(_ptr(x), M, K, *g, *u, N, _ptr(h), _stream(x.device)))
+    elif M >= GEMM_MIN_M:
+        n = rms_norm(x, norm_weight, eps)
+        _check(lib().mq4_mlp_gate_up_silu(_ptr(n), M, K, *g, *u, N, _ptr(h), _stream(x.device)))
     else:
         norm_weight = _need(norm_weight, torch.bfloat16, "norm_weight")
         _check(lib().mq4_rmsnorm_gate_up_silu(_ptr(x), M, K, _ptr(norm_weight), eps, *g, *u, N, _ptr(h),

@@ -167,6 +167,17 @@ def test_gemm_epilogues_at_prefill_m(mq4, O, dev):
     _, gbn = O.qmm_f64(n, *gh)
     _, ubn = O.qmm_f64(n, *uh)
     check_swiglu(O, to_host_u16(hn)[rows], O.swiglu_bf16(gbn, ubn), "prefill norm+SwiGLU")
+    # the C entry point with the norm fused into the GEMM (what the Python
+    # binding replaces by two launches at this size)
+    import ctypes
+    hc = torch.empty_like(hn)
+    P = ctypes.c_void_p
+    rc = mq4.lib().mq4_rmsnorm_gate_up_silu(P(x.data_ptr()), M, K, P(nw.data_ptr()), ctypes.c_float(1e-6),
+                                            *[P(t.data_ptr()) for t in g], *[P(t.data_ptr()) for t in u], N,
+                                            P(hc.data_ptr()), None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    check_swiglu(O, to_host_u16(hc)[rows], O.swiglu_bf16(gbn, ubn), "prefill norm+SwiGLU (fused C entry)")
 
     # down projection of h with the residual add (src/model/marlin.cpp:142)
     (d, dh) = make(mq4, O, K, N, 1002, dev)
