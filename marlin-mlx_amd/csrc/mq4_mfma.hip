@@ -371,69 +371,95 @@ __global__ __launch_bounds__(64 * KS) void q4_mfma_gemv_kernel(GemvParams p) {
 
 namespace {
 
+// Workgroups of `kernel` (64 * KS threads) that one CU holds at once, from the
+// runtime's occupancy calculation; cached per kernel instance.
+template <int KS>
+int resident_per_cu(const void* kernel, int& cache) {
+    if (cache == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 64 * KS, 0) != hipSuccess || n < 1) n = 1;
+        cache = n;
+    }
+    return cache;
+}
+
+template <int MT, int GW, int KS, int NMAT, int EPI, bool NORM, bool XREG, bool PF, bool SBV>
+void launch_one(const GemvParams& a, int tiles, hipStream_t st) {
+    // The grid never exceeds what the GPU holds at once: a second batch of
+    // workgroups would start only as the first drains.  Workgroups loop over
+    // tiles (blockIdx.x + r * gridDim.x) instead.
+    static int per_cu = 0;
+    auto* k = mf::q4_mfma_gemv_kernel<MT, GW, KS, NMAT, EPI, NORM, XREG, PF, SBV>;
+    int grid = resident_per_cu<KS>(reinterpret_cast<const void*>(k), per_cu) * num_cus();
+    if (grid > tiles) grid = tiles;
+    if (EPI == EPI_ARGMAX && grid > kPartialStride) grid = kPartialStride;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * KS), 0, st, a);
+    if (EPI == EPI_ARGMAX) launch_argmax_finalize(a.partial, grid, a.m_valid, a.idx, st);
+}
+
 template <int MT, int GW, int KS, int NMAT, int EPI, bool NORM, bool XREG>
-void launch(const GemvParams& a, int grid, hipStream_t st) {
-    // PF: several rounds per block, the next round's weights in flight;
-    // SBV: vector scale/bias loads (whole rows of GW groups, aligned)
+void launch(const GemvParams& a, hipStream_t st) {
+    // PF: the next tile's weights in flight while the current one is reduced
+    // (when workgroups loop over several tiles); SBV: vector scale/bias loads
+    // (whole rows of GW groups, aligned)
     const int tiles = (a.N + 15) / 16;
     const int G = a.K / 64;
-    constexpr bool kCanPF = KS <= 4 && NMAT == 1;    // registers for a second weight buffer
-    const bool pf = kCanPF && tiles > grid;
-    const bool sbv = G % 8 == 0 && aligned(a.A.s, 16) && aligned(a.A.b, 16) &&
+    constexpr bool kCanPF = NMAT == 1 && (KS <= 4 || GW <= 4);   // registers for a second weight buffer
+    const bool pf = kCanPF && tiles > num_cus();
+    const bool sbv = G % GW == 0 && aligned(a.A.s, 16) && aligned(a.A.b, 16) &&
                      (NMAT == 1 || (aligned(a.B.s, 16) && aligned(a.B.b, 16)));
-    const dim3 g((unsigned)grid), b(64 * KS);
     if constexpr (kCanPF) {
         if (pf) {
-            if (sbv) hipLaunchKernelGGL((mf::q4_mfma_gemv_kernel<MT, GW, KS, NMAT, EPI, NORM, XREG, true, true>), g, b, 0, st, a);
-            else hipLaunchKernelGGL((mf::q4_mfma_gemv_kernel<MT, GW, KS, NMAT, EPI, NORM, XREG, true, false>), g, b, 0, st, a);
+            if (sbv) launch_one<MT, GW, KS, NMAT, EPI, NORM, XREG, true, true>(a, tiles, st);
+            else launch_one<MT, GW, KS, NMAT, EPI, NORM, XREG, true, false>(a, tiles, st);
             return;
         }
     }
-    {
-        if (sbv) hipLaunchKernelGGL((mf::q4_mfma_gemv_kernel<MT, GW, KS, NMAT, EPI, NORM, XREG, false, true>), g, b, 0, st, a);
-        else hipLaunchKernelGGL((mf::q4_mfma_gemv_kernel<MT, GW, KS, NMAT, EPI, NORM, XREG, false, false>), g, b, 0, st, a);
-    }
+    if (sbv) launch_one<MT, GW, KS, NMAT, EPI, NORM, XREG, false, true>(a, tiles, st);
+    else launch_one<MT, GW, KS, NMAT, EPI, NORM, XREG, false, false>(a, tiles, st);
 }
 
 // (MT, GW, XREG) fixed per shape class; KS = the smallest provided wave count
 // covering all G groups, at most MAXKS (more waves per block would leave too
 // few registers per lane and spill).
 template <int MT, int GW, int MAXKS, int NMAT, int EPI, bool NORM, bool XREG>
-int dispatch_ks(const GemvParams& a, int grid, hipStream_t st) {
+int dispatch_ks(const GemvParams& a, hipStream_t st) {
     const int G = a.K / 64;
     const int need = (G + GW - 1) / GW;
-    if (need <= 1) { launch<MT, GW, 1, NMAT, EPI, NORM, XREG>(a, grid, st); return 0; }
-    if (need <= 2) { launch<MT, GW, 2, NMAT, EPI, NORM, XREG>(a, grid, st); return 0; }
-    if (need <= 4) { launch<MT, GW, 4, NMAT, EPI, NORM, XREG>(a, grid, st); return 0; }
+    if (need <= 1) { launch<MT, GW, 1, NMAT, EPI, NORM, XREG>(a, st); return 0; }
+    if (need <= 2) { launch<MT, GW, 2, NMAT, EPI, NORM, XREG>(a, st); return 0; }
+    if (need <= 4) { launch<MT, GW, 4, NMAT, EPI, NORM, XREG>(a, st); return 0; }
     if constexpr (MAXKS >= 8) {
-        if (need <= 8) { launch<MT, GW, 8, NMAT, EPI, NORM, XREG>(a, grid, st); return 0; }
+        if (need <= 8) { launch<MT, GW, 8, NMAT, EPI, NORM, XREG>(a, st); return 0; }
     }
     if constexpr (MAXKS >= 12) {
-        if (need <= 12) { launch<MT, GW, 12, NMAT, EPI, NORM, XREG>(a, grid, st); return 0; }
+        if (need <= 12) { launch<MT, GW, 12, NMAT, EPI, NORM, XREG>(a, st); return 0; }
     }
     return -1;
 }
 
 template <int EPI, bool NORM>
-int dispatch(const GemvParams& a, int grid, hipStream_t st) {
+int dispatch(const GemvParams& a, hipStream_t st) {
     constexpr int NMAT = EPI == EPI_SWIGLU ? 2 : 1;
     const int G = a.K / 64;
     if (NORM && a.K > 2048) return -1;                 // the LDS copy of the norm weights holds K <= 2048
     if (a.m_valid <= 16) {
-        // 8 groups per wave, activations in registers (64 VGPRs): K <= 6144
-        // for single-matrix stores, K <= 4096 for the fused SwiGLU and argmax
-        // epilogues and K <= 2048 for norm + SwiGLU (more waves per block
-        // would leave too few registers per lane)
+        // Up to K = 2048: 4 groups per wave over up to 8 waves (activations
+        // in registers, 32 VGPRs; about 115 VGPRs per lane, two 8-wave
+        // workgroups per CU).  Beyond: 8 groups per wave (64 VGPRs) up to
+        // K = 6144 for single-matrix stores and K = 4096 for the fused SwiGLU
+        // and argmax epilogues.
+        if (G <= 8 * 4) return dispatch_ks<1, 4, 8, NMAT, EPI, NORM, true>(a, st);
         constexpr int MAXKS = (NORM && NMAT == 2) ? 4 : (NMAT == 2 || EPI == EPI_ARGMAX) ? 8 : 12;
-        if (G <= MAXKS * 8) return dispatch_ks<1, 8, MAXKS, NMAT, EPI, NORM, true>(a, grid, st);
+        if (G <= MAXKS * 8) return dispatch_ks<1, 8, MAXKS, NMAT, EPI, NORM, true>(a, st);
         return -1;
     }
     // two 16-row activation tiles: 4 groups per wave in registers up to
     // K = 2048; beyond, for the single-matrix stores, 8 groups per wave re-read
     // from L2 up to K = 6144.  Other shapes return -1 (the dot2 GEMV runs them).
-    if (G <= 8 * 4) return dispatch_ks<2, 4, 8, NMAT, EPI, NORM, true>(a, grid, st);
+    if (G <= 8 * 4) return dispatch_ks<2, 4, 8, NMAT, EPI, NORM, true>(a, st);
     if constexpr (!NORM && NMAT == 1 && EPI != EPI_ARGMAX) {
-        if (G <= 12 * 8) return dispatch_ks<2, 8, 12, NMAT, EPI, false, false>(a, grid, st);
+        if (G <= 12 * 8) return dispatch_ks<2, 8, 12, NMAT, EPI, false, false>(a, st);
     }
     return -1;
 }
@@ -442,23 +468,15 @@ int dispatch(const GemvParams& a, int grid, hipStream_t st) {
 
 int launch_q4_mfma_gemv(const GemvParams& a, int epi, bool norm, hipStream_t st) {
     if (a.m_valid < 1 || a.m_valid > kMfmaMaxM) return -1;
-    const int tiles = (a.N + 15) / 16;
-    // one round per block unless the matrix is large; the argmax keeps at
-    // most kPartialStride per-block partial keys per row
-    int grid = tiles;
-    const int cap = epi == EPI_ARGMAX ? num_cus() * 4 : num_cus() * 8;
-    if (grid > cap) grid = cap;
-    if (grid > kPartialStride) grid = kPartialStride;
     int rc = -1;
     switch (epi) {
-        case EPI_STORE: rc = norm ? -1 : dispatch<EPI_STORE, false>(a, grid, st); break;
-        case EPI_STORE_F32: rc = norm ? -1 : dispatch<EPI_STORE_F32, false>(a, grid, st); break;
-        case EPI_RESIDUAL: rc = norm ? -1 : dispatch<EPI_RESIDUAL, false>(a, grid, st); break;
-        case EPI_SWIGLU: rc = norm ? dispatch<EPI_SWIGLU, true>(a, grid, st) : dispatch<EPI_SWIGLU, false>(a, grid, st); break;
-        case EPI_ARGMAX: rc = norm ? dispatch<EPI_ARGMAX, true>(a, grid, st) : dispatch<EPI_ARGMAX, false>(a, grid, st); break;
+        case EPI_STORE: rc = norm ? -1 : dispatch<EPI_STORE, false>(a, st); break;
+        case EPI_STORE_F32: rc = norm ? -1 : dispatch<EPI_STORE_F32, false>(a, st); break;
+        case EPI_RESIDUAL: rc = norm ? -1 : dispatch<EPI_RESIDUAL, false>(a, st); break;
+        case EPI_SWIGLU: rc = norm ? dispatch<EPI_SWIGLU, true>(a, st) : dispatch<EPI_SWIGLU, false>(a, st); break;
+        case EPI_ARGMAX: rc = norm ? dispatch<EPI_ARGMAX, true>(a, st) : dispatch<EPI_ARGMAX, false>(a, st); break;
         default: rc = -1;
     }
-    if (rc == 0 && epi == EPI_ARGMAX) launch_argmax_finalize(a.partial, grid, a.m_valid, a.idx, st);
     return rc;
 }
 
