@@ -39,9 +39,19 @@ CFLAGS = [
 ]
 
 
+# Per-source extra flags.  mq4_gemm.hip: MFMA results and accumulators in
+# VGPRs (-amdgpu-mfma-vgpr-form).  Its per-group fold (acc += s * D) is VALU
+# work on the MFMA results; with them in AGPRs every group moved 128 values
+# between AGPRs and VGPRs (v_accvgpr_read/write), half the loop's VALU
+# instructions.
+EXTRA_FLAGS = {
+    "mq4_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass does not know the packed-fp32 feature; that notice is harmless.
     err = "\n".join(l for l in p.stderr.splitlines() if "packed-fp32-ops" not in l)

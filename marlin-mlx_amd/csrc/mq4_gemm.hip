@@ -61,6 +61,19 @@ constexpr int LDS_STRIDE = 72;          // bf16 per LDS row (64 activations + 8 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
+// This file is built with MFMA results and accumulators in VGPRs
+// (-amdgpu-mfma-vgpr-form), so the per-group fold reads the MFMA result D
+// directly on the VALU.  The compiler pads each v_mfma_f32_32x32x16_bf16 ->
+// VALU read with 11 wait states, which measured too few on gfx950 (the sums
+// came out wrong); 24 more, once per group between the group's last MFMA and
+// its fold, give the right sums at no measurable cost.  The scheduling
+// barriers keep the padding between the two.
+__device__ __forceinline__ void mfma_result_pad() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ bf16x8_t weight_operand(uint32_t word) {
     const uint4 q = make_uint4(nib_pair_bf16<0>(word), nib_pair_bf16<1>(word), nib_pair_bf16<2>(word),
                                nib_pair_bf16<3>(word));
@@ -218,6 +231,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm_kernel(GemmArgs p) {
                 for (int j = 0; j < 2; ++j)
                     D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], ks == 0 ? zero : D[i][j], 0, 0, 0);
         }
+        mfma_result_pad();
         // fold the group: acc += s * D + (b - 128 s) * X
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -459,6 +473,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q4_gemm_dma_kernel(GemmArgs p
                 for (int j = 0; j < 2; ++j)
                     D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], ks == 0 ? zero : D[i][j], 0, 0, 0);
         }
+        mfma_result_pad();
         float X[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) X[i] = xs[i] + __shfl_xor(xs[i], 32);
