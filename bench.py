@@ -609,31 +609,56 @@ def bench_sampling(E, lm, norm_w, x0):
 def bench_pack(E, layers, lm):
     """Config 5b: quantize/pack of the full weight set (72 MLP matrices + the
     lm_head).  The bf16 weights are generated again (the same streams as the
-    setup), then all 73 mq4_quantize calls are launched back to back between
-    one pair of HIP events (median of 3 passes); the packed output must equal
-    the setup's bit for bit.  The setup's per-matrix timings (an event pair and
-    a synchronize around each call, so each includes the launch gap) are
-    reported beside it."""
+    setup) and packed by mq4_quantize_batch (the loader's whole loop in three
+    launches of at most 32 matrices) between one pair of HIP events (median of
+    3 passes); the same 73 matrices as 73 mq4_quantize calls back to back are
+    timed beside it.  Both outputs must equal the setup's bit for bit.  The
+    setup's per-matrix timings (an event pair and a synchronize around each
+    call) are reported too."""
     torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
     srcs = [(mq4.fill_normal_bf16(shape, sid, 0.0, 0.02, device=E.dev), shape) for shape, sid in E.pack_set]
-    outs = [(torch.empty((N, K // 8), dtype=torch.int32, device=E.dev),
-             torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev),
-             torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev)) for _, (N, K) in srcs]
-    st = E.st()
 
-    def pack_all():
+    def fresh():
+        return [(torch.empty((N, K // 8), dtype=torch.int32, device=E.dev),
+                 torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev),
+                 torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev)) for _, (N, K) in srcs]
+
+    st = E.st()
+    ref = [q for lay in layers for q in lay] + [lm]
+
+    def same_as_setup(outs):
+        return all(torch.equal(o[0], r.wq) and torch.equal(o[1], r.s) and torch.equal(o[2], r.b)
+                   for o, r in zip(outs, ref))
+
+    outs = fresh()
+
+    def pack_separate():
         for (w, (N, K)), (wq, s, b) in zip(srcs, outs):
             L.mq4_quantize(P(w.data_ptr()), N, K, 64, 4, P(wq.data_ptr()), P(s.data_ptr()), P(b.data_ptr()), st)
 
-    us = statistics.median([E.timed(pack_all, 1, warm=1 if i == 0 else 0) for i in range(3)])
-    ref = [q for lay in layers for q in lay] + [lm]
-    same = all(torch.equal(o[0], r.wq) and torch.equal(o[1], r.s) and torch.equal(o[2], r.b) for o, r in zip(outs, ref))
-    del srcs, outs
+    us_sep = statistics.median([E.timed(pack_separate, 1, warm=1 if i == 0 else 0) for i in range(3)])
+    same_sep = same_as_setup(outs)
+
+    outs_b = fresh()
+    jobs = (mq4._QuantJobC * len(srcs))()
+    for i, ((w, (N, K)), (wq, s, b)) in enumerate(zip(srcs, outs_b)):
+        jobs[i] = mq4._QuantJobC(w.data_ptr(), N, K, wq.data_ptr(), s.data_ptr(), b.data_ptr())
+    jobs_p = ctypes.cast(jobs, ctypes.c_void_p)
+
+    def pack_batch():
+        mq4._check(L.mq4_quantize_batch(jobs_p, len(srcs), 64, 4, st))
+
+    us = statistics.median([E.timed(pack_batch, 1, warm=1 if i == 0 else 0) for i in range(3)])
+    same = same_as_setup(outs_b)
+    del srcs, outs, outs_b
     return {"bytes": E.pack_bytes, "us": round(us, 1), "roofline": hbm_roofline(E.pack_bytes, us),
-            "bit_identical_to_setup": bool(same),
+            "bit_identical_to_setup": bool(same and same_sep),
+            "separate_calls_us": round(us_sep, 1),
+            "separate_calls_roofline": hbm_roofline(E.pack_bytes, us_sep),
             "per_matrix_sum_us": round(E.pack_us, 1),
             "note": "read 2 B per bf16 weight + write 0.5625 B per weight (words, scales, biases); "
-                    "73 calls back to back between one event pair, median of 3 passes"}
+                    "mq4_quantize_batch over the 73 matrices (3 launches) between one event pair, median of 3 "
+                    "passes; separate_calls_us: the same 73 matrices as 73 mq4_quantize calls back to back"}
 
 
 # ----------------------------------------------------------- profile modes
@@ -683,7 +708,19 @@ def profile_mode(args, E, layers, lm, norm_w, layer_norms, x0, dstep, dargs):
             L.mq4_rmsnorm_lm_head_argmax(P(x.data_ptr()), M, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB,
                                          P(idx.data_ptr()), None, P(ws.data_ptr()), wsb, st)
     elif k == "pack":
-        pass                                   # the setup above packed the full weight set once
+        # the setup above packed the full weight set matrix by matrix; here the
+        # same set goes through mq4_quantize_batch warmup + steps times
+        srcs = [(mq4.fill_normal_bf16(shape, sid, 0.0, 0.02, device=E.dev), shape) for shape, sid in E.pack_set]
+        jobs = (mq4._QuantJobC * len(srcs))()
+        keep = []
+        for i, (w, (N, K)) in enumerate(srcs):
+            o = (torch.empty((N, K // 8), dtype=torch.int32, device=E.dev),
+                 torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev),
+                 torch.empty((N, K // 64), dtype=torch.bfloat16, device=E.dev))
+            keep.append(o)
+            jobs[i] = mq4._QuantJobC(w.data_ptr(), N, K, o[0].data_ptr(), o[1].data_ptr(), o[2].data_ptr())
+        for _ in range(n):
+            mq4._check(L.mq4_quantize_batch(ctypes.cast(jobs, ctypes.c_void_p), len(srcs), 64, 4, st))
     torch.cuda.synchronize()
     log(f"[bench] profile {k}: {n} iterations")
 

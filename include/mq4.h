@@ -24,6 +24,8 @@
  *   mq4_quantize         mx::quantize(w, 64, 4) in quantize_weight
  *                        (src/model/weights.cpp:45-56) and the lm_head load
  *                        (src/model/weights.cpp:180-194)
+ *   mq4_quantize_batch   the loader's loop of those quantizes over every
+ *                        layer (src/model/weights.cpp:97-104, 147-160, 180-194)
  *   mq4_qmm              mx::quantized_matmul(x, w, s, b, true, 64, 4) in
  *                        qmatmul (src/model/marlin.cpp:18-25) and
  *                        MarlinModel::lm_head (src/model/marlin.cpp:161-169)
@@ -82,6 +84,27 @@ int mq4_version(void);
  * w must be 16-byte aligned, wq 4-byte, scales/biases 2-byte. */
 int mq4_quantize(const uint16_t* w, int64_t N, int64_t K, int group_size, int bits,
                  uint32_t* wq, uint16_t* scales, uint16_t* biases, void* stream);
+
+/* One matrix of a batched quantize: w bf16 [N, K] in, wq/scales/biases out,
+ * the same layout and alignment as mq4_quantize. */
+typedef struct mq4_quantize_job {
+    const uint16_t* w;
+    int64_t N, K;
+    uint32_t* wq;
+    uint16_t* scales;
+    uint16_t* biases;
+} mq4_quantize_job;
+
+/* Quantize every job of a weight set in as few launches as possible (one per
+ * 32 jobs), with the same bits as n_jobs separate mq4_quantize calls.
+ * Replaces the loader's loop of quantizes: quantize_weight for gate, up and
+ * down of every layer (load_mlp, src/model/weights.cpp:97-104, called per
+ * layer at :147-160) and the lm_head's mx::quantize (:180-194).  The job
+ * table is read on the host during the call; every job is validated before
+ * anything is enqueued (on an error nothing runs and the message names the
+ * job).  Jobs must not overlap in their outputs. */
+int mq4_quantize_batch(const mq4_quantize_job* jobs, int64_t n_jobs, int group_size, int bits,
+                       void* stream);
 
 /* Dequantize: out = scales*q + biases, rounded once (round-to-nearest-even)
  * to bf16 (out_f32 == 0, out is uint16_t*) or stored exactly as float

@@ -30,7 +30,7 @@ import torch
 __all__ = [
     "MQ4Error", "library_path", "lib", "QuantizedTensor", "MLPWeights",
     "quantize", "dequantize", "quantized_matmul", "quantized_matmul_f32", "argmax", "swiglu",
-    "quantize_weight", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
+    "quantize_weight", "quantize_batch", "quantize_weights", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
     "lm_head", "lm_head_argmax", "lm_head_last_row", "sample_token", "rms_norm", "fill_normal_bf16",
     "DecoderLayer", "DecodeStep", "save_q4_cache", "load_q4_cache", "quantize_or_load",
 ]
@@ -95,6 +95,7 @@ def lib():
         "mq4_last_error": ([], ctypes.c_char_p),
         "mq4_version": ([], I),
         "mq4_quantize": ([P, I64, I64, I, I, P, P, P, P], I),
+        "mq4_quantize_batch": ([P, I64, I, I, P], I),
         "mq4_dequantize": ([P, P, P, I64, I64, I, I, P, I, P], I),
         "mq4_qmm": ([P, I64, I64, P, P, P, I64, I, I, I, P, P], I),
         "mq4_qmm_residual": ([P, I64, I64, P, P, P, I64, P, P, P], I),
@@ -206,6 +207,46 @@ def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4):
     _check(lib().mq4_quantize(_ptr(w), N, K, group_size, bits, _ptr(wq), _ptr(s), _ptr(b),
                               _stream(w.device)))
     return wq, s, b
+
+
+class _QuantJobC(ctypes.Structure):
+    """mq4_quantize_job (include/mq4.h)."""
+    _fields_ = [("w", ctypes.c_void_p), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+                ("wq", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p)]
+
+
+def quantize_batch(ws, group_size: int = 64, bits: int = 4):
+    """mx::quantize over a whole weight set in one batched call: the loader's
+    loop of quantize_weight calls (src/model/weights.cpp:97-104, 147-160) plus
+    the lm_head's (:180-194).  ws: bf16 tensors [..., K] on one device (K may
+    differ between them).  Returns a list of (wq, scales, biases), bit for bit
+    what quantize() returns for each."""
+    fn = "quantize_batch"
+    ws = list(ws)
+    if not ws:
+        return []
+    dev = ws[0].device
+    jobs = (_QuantJobC * len(ws))()
+    outs = []
+    for i, w in enumerate(ws):
+        w = _need(w, torch.bfloat16, f"ws[{i}]")
+        if w.device != dev:
+            raise ValueError(f"{fn}: every weight must be on {dev} (ws[{i}] is on {w.device})")
+        K = w.shape[-1]
+        lead = w.shape[:-1]
+        wq = torch.empty((*lead, K // 8), dtype=torch.int32, device=dev)
+        s = torch.empty((*lead, K // max(group_size, 1)), dtype=torch.bfloat16, device=dev)
+        b = torch.empty_like(s)
+        jobs[i] = _QuantJobC(_ptr(w), w.numel() // K if K else 0, K, _ptr(wq), _ptr(s), _ptr(b))
+        outs.append((w, wq, s, b))
+    _check(lib().mq4_quantize_batch(ctypes.cast(jobs, ctypes.c_void_p), len(ws), group_size, bits, _stream(dev)))
+    return [(wq, s, b) for (_, wq, s, b) in outs]
+
+
+def quantize_weights(ws, bits: int = 4, group_size: int = 64) -> list:
+    """quantize_weight (src/model/weights.cpp:45-56) for a list of bf16 [N, K]
+    weights in one batched call; returns QuantizedTensors."""
+    return [QuantizedTensor(wq, s, b, group_size, bits, True) for wq, s, b in quantize_batch(ws, group_size, bits)]
 
 
 def dequantize(wq: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,

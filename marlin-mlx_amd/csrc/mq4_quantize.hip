@@ -94,14 +94,12 @@ __device__ __forceinline__ void pack16(const uint4* v, uint32_t* word, float* sc
     *bias_out = bias;
 }
 
-// Each lane packs two consecutive words (16 weights) per step and takes two
-// steps per loop iteration, with all four 16-byte loads issued first.
-__global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w,
-                                                           int64_t n_words,
-                                                           uint32_t* __restrict__ wq,
-                                                           uint16_t* __restrict__ scales,
-                                                           uint16_t* __restrict__ biases) {
-    const int64_t n_pairs = n_words >> 1;
+// Grid-stride pass over one flat stream of n_pairs word pairs: each lane
+// packs two consecutive words (16 weights) per step and takes two steps per
+// loop iteration, with all four 16-byte loads issued first.
+__device__ __forceinline__ void quantize_stream(const uint4* __restrict__ w, int64_t n_pairs,
+                                                uint32_t* __restrict__ wq, uint16_t* __restrict__ scales,
+                                                uint16_t* __restrict__ biases) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     // The loop bound is block-uniform so the cross-lane reductions run with
     // every lane of the wave active.
@@ -132,6 +130,31 @@ __global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restri
             }
         }
     }
+}
+
+__global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w, int64_t n_words,
+                                                           uint32_t* __restrict__ wq,
+                                                           uint16_t* __restrict__ scales,
+                                                           uint16_t* __restrict__ biases) {
+    quantize_stream(w, n_words >> 1, wq, scales, biases);
+}
+
+// Several matrices in one launch: the jobs' flat streams one after the other
+// (every workgroup takes its share of job j, then moves on to job j + 1
+// without waiting for the others), so the launch ramp and tail are paid once
+// instead of per matrix.  The job table travels in the kernel arguments.
+constexpr int kQuantBatch = 32;
+struct QuantBatch {
+    const uint4* w[kQuantBatch];
+    uint32_t* wq[kQuantBatch];
+    uint16_t* s[kQuantBatch];
+    uint16_t* b[kQuantBatch];
+    int64_t n_pairs[kQuantBatch];
+    int n;
+};
+
+__global__ __launch_bounds__(256) void quantize_g64_batch_kernel(QuantBatch a) {
+    for (int j = 0; j < a.n; ++j) quantize_stream(a.w[j], a.n_pairs[j], a.wq[j], a.s[j], a.b[j]);
 }
 
 // One packed word per lane: 8 outputs = scale * q + bias (q * scale is exact
@@ -239,6 +262,48 @@ extern "C" int mq4_quantize(const uint16_t* w, int64_t N, int64_t K, int group_s
     hipLaunchKernelGGL(quantize_g64_kernel, dim3(grid), dim3(block), 0, as_stream(stream),
                        reinterpret_cast<const uint4*>(w), n_words, wq, scales, biases);
     return launch_status(what);
+}
+
+extern "C" int mq4_quantize_batch(const mq4_quantize_job* jobs, int64_t n_jobs, int group_size, int bits,
+                                  void* stream) {
+    const char* what = "mq4_quantize_batch";
+    if (int rc = check_format(what, group_size, bits)) return rc;
+    if (n_jobs < 0 || (n_jobs > 0 && !jobs))
+        return fail(MQ4_ERR_INVALID_ARG, "%s: n_jobs=%lld with %s job table", what, (long long)n_jobs,
+                    jobs ? "a" : "no");
+    for (int64_t j = 0; j < n_jobs; ++j) {
+        const mq4_quantize_job& q = jobs[j];
+        if (q.K <= 0 || q.K % 64 != 0)
+            return fail(MQ4_ERR_INVALID_ARG, "%s: job %lld: K=%lld must be a positive multiple of 64", what,
+                        (long long)j, (long long)q.K);
+        if (q.N <= 0) return fail(MQ4_ERR_INVALID_ARG, "%s: job %lld: N=%lld must be positive", what, (long long)j,
+                                  (long long)q.N);
+        if (!q.w || !q.wq || !q.scales || !q.biases)
+            return fail(MQ4_ERR_INVALID_ARG, "%s: job %lld: null pointer", what, (long long)j);
+        if (!aligned(q.w, 16) || !aligned(q.wq, 4) || !aligned(q.scales, 2) || !aligned(q.biases, 2))
+            return fail(MQ4_ERR_ALIGNMENT,
+                        "%s: job %lld: w must be 16-byte aligned, wq 4-byte, scales/biases 2-byte", what,
+                        (long long)j);
+    }
+    for (int64_t j0 = 0; j0 < n_jobs; j0 += kQuantBatch) {
+        QuantBatch a{};
+        a.n = (int)((n_jobs - j0) < kQuantBatch ? (n_jobs - j0) : kQuantBatch);
+        for (int i = 0; i < a.n; ++i) {
+            const mq4_quantize_job& q = jobs[j0 + i];
+            a.w[i] = reinterpret_cast<const uint4*>(q.w);
+            a.wq[i] = q.wq;
+            a.s[i] = q.scales;
+            a.b[i] = q.biases;
+            a.n_pairs[i] = q.N * (q.K / 16);
+        }
+        // enough lanes to keep HBM busy, not more than the largest job uses
+        int64_t largest = 0;
+        for (int i = 0; i < a.n; ++i) largest = a.n_pairs[i] > largest ? a.n_pairs[i] : largest;
+        const int grid = grid_for((largest + 1) / 2, 256, 256 * 32);
+        hipLaunchKernelGGL(quantize_g64_batch_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a);
+        if (int rc = launch_status(what)) return rc;
+    }
+    return ok();
 }
 
 extern "C" int mq4_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,

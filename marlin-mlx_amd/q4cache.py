@@ -130,12 +130,13 @@ def load_q4_cache(path: str, device="cuda", group_size: int | None = None, bits:
 def quantize_or_load(path: str, weights: dict, device="cuda") -> dict:
     """The load-time step of the reference (quantize each bf16 weight) with a
     cache: if `path` exists and holds every name, load it; otherwise quantize
-    the given bf16 [N, K] tensors and write the cache."""
-    from . import quantize_weight
+    the given bf16 [N, K] tensors (one batched quantize) and write the cache."""
+    from . import quantize_weights
     if os.path.exists(path):
         cached = load_q4_cache(path, device)
         if all(n in cached for n in weights):
             return {n: cached[n] for n in weights}
-    out = {n: quantize_weight(w) for n, w in weights.items()}
+    names = list(weights)
+    out = dict(zip(names, quantize_weights([weights[n] for n in names])))
     save_q4_cache(path, out)
     return out

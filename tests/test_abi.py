@@ -59,6 +59,28 @@ def test_quantize_validation(mq4):
     assert L.mq4_quantize(fake(A16), 4, 128, 64, 4, fake(A16 + 2), fake(A16), fake(A16), S) == ALIGN
 
 
+def test_quantize_batch_validation(mq4):
+    """Every job is checked before anything is enqueued; the message names the
+    failing job.  (n_jobs = 0 is a no-op that enqueues nothing.)"""
+    L = mq4.lib()
+    good = mq4._QuantJobC(A16, 4, 128, A16, A16, A16)
+    table = (mq4._QuantJobC * 3)(good, mq4._QuantJobC(A16, 4, 96, A16, A16, A16), good)
+    jobs = ctypes.cast(table, ctypes.c_void_p)
+    assert L.mq4_quantize_batch(jobs, 3, 64, 4, S) == INVALID
+    assert "job 1" in last_error(mq4) and "K=96" in last_error(mq4)
+    table[1] = mq4._QuantJobC(A16, 0, 128, A16, A16, A16)
+    assert L.mq4_quantize_batch(jobs, 3, 64, 4, S) == INVALID and "job 1" in last_error(mq4)
+    table[1] = mq4._QuantJobC(A16 + 8, 4, 128, A16, A16, A16)
+    assert L.mq4_quantize_batch(jobs, 3, 64, 4, S) == ALIGN
+    table[1] = mq4._QuantJobC(A16, 4, 128, None, A16, A16)
+    assert L.mq4_quantize_batch(jobs, 3, 64, 4, S) == INVALID
+    table[1] = good
+    assert L.mq4_quantize_batch(jobs, 3, 32, 4, S) == UNSUPPORTED
+    assert L.mq4_quantize_batch(jobs, -1, 64, 4, S) == INVALID
+    assert L.mq4_quantize_batch(None, 2, 64, 4, S) == INVALID
+    assert L.mq4_quantize_batch(None, 0, 64, 4, S) == OK
+
+
 def test_qmm_validation(mq4):
     L = mq4.lib()
     args = lambda **kw: [kw.get("x", fake(A16)), kw.get("M", 1), kw.get("K", 2048), kw.get("wq", fake(A16)),

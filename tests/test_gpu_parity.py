@@ -162,6 +162,30 @@ def test_quantize_quotients_at_half_integers(mq4, O, dev):
     assert np.array_equal(words(wq), rq)
 
 
+def test_quantize_batch_matches_oracle(mq4, O, dev):
+    """mq4_quantize_batch over 41 jobs of mixed shapes (two launches of at most
+    32 jobs; K differs between jobs; ragged N): every job bit-identical to the
+    oracle and to its own mq4_quantize call."""
+    rng = np.random.default_rng(21)
+    shapes = [(6144, 2048), (2048, 6144), (1, 64), (3, 192), (7, 4160)]
+    shapes += [(int(rng.integers(1, 300)), 64 * int(rng.integers(1, 40))) for _ in range(36)]
+    ws, whs = [], []
+    for i, (N, K) in enumerate(shapes):
+        w, wh = gen_weight(mq4, O, 3000 + i, N, K)
+        ws.append(w)
+        whs.append(wh)
+    print(f"quantize_batch {len(shapes)} jobs", flush=True)
+    outs = mq4.quantize_batch(ws)
+    torch.cuda.synchronize()
+    for i, ((wq, s, b), w, wh) in enumerate(zip(outs, ws, whs)):
+        rq, rs, rb = O.quantize(wh)
+        assert np.array_equal(words(wq), rq), i
+        assert np.array_equal(to_host_u16(s), rs), i
+        assert np.array_equal(to_host_u16(b), rb), i
+        sq, ss, sb = mq4.quantize(w)
+        assert torch.equal(sq, wq) and torch.equal(ss, s) and torch.equal(sb, b), i
+
+
 def test_dequantize_matches_affine_formula(mq4, O, dev):
     N, K = 96, 2048
     w, wh = gen_weight(mq4, O, 9, N, K)
