@@ -4,6 +4,7 @@
 //
 //   marlin::QuantizedTensor      src/core/types.h:75-82
 //   quantize_weight              src/model/weights.cpp:45-56 (:180-194 lm_head)
+//   quantize_weights             the loader loop of those, src/model/weights.cpp:97-104, 147-160
 //   qmatmul                      src/model/marlin.cpp:18-25
 //   mlp_forward                  src/model/marlin.cpp:31-35 (+ :141-142)
 //   lm_head                      src/model/marlin.cpp:161-169
@@ -22,6 +23,7 @@
 #include <string>
 #include <utility>
 #include <variant>
+#include <vector>
 
 #include "mq4.h"
 
@@ -119,6 +121,42 @@ inline Result<QuantizedTensor> quantize_weight(const uint16_t* w, int64_t N, int
     if (rc != MQ4_OK) return last_error(rc);
     q.quantized = true;
     return q;
+}
+
+// A bf16 [N, K] device weight to quantize (quantize_weights).
+struct WeightView {
+    const uint16_t* w;
+    int64_t N, K;
+};
+
+// The loader's loop of quantize_weight calls (src/model/weights.cpp:97-104
+// per layer at :147-160, and the lm_head at :180-194) as one batched call
+// (mq4_quantize_batch); the tensors are bit-identical to quantize_weight's.
+inline Result<std::vector<QuantizedTensor>> quantize_weights(const std::vector<WeightView>& ws,
+                                                             hipStream_t stream, int bits = 4,
+                                                             int group_size = 64) {
+    std::vector<QuantizedTensor> out(ws.size());
+    std::vector<mq4_quantize_job> jobs(ws.size());
+    const int64_t gs = group_size > 0 ? group_size : 1;
+    for (size_t i = 0; i < ws.size(); ++i) {
+        QuantizedTensor& q = out[i];
+        q.out_features = ws[i].N;
+        q.in_features = ws[i].K;
+        q.bits = bits;
+        q.group_size = group_size;
+        const bool shape_ok = ws[i].N > 0 && ws[i].K > 0;
+        q.weight = DeviceBuffer(shape_ok ? (size_t)ws[i].N * (size_t)ws[i].K / 8 * 4 : 0);
+        q.scales = DeviceBuffer(shape_ok ? (size_t)ws[i].N * (size_t)(ws[i].K / gs) * 2 : 0);
+        q.biases = DeviceBuffer(q.scales.bytes());
+        if (shape_ok && (!q.weight.get() || !q.scales.get() || !q.biases.get()))
+            return Error{MQ4_ERR_HIP, "quantize_weights: device allocation failed"};
+        jobs[i] = mq4_quantize_job{ws[i].w, ws[i].N, ws[i].K, q.weight.as<uint32_t>(), q.scales.as<uint16_t>(),
+                                   q.biases.as<uint16_t>()};
+    }
+    const int rc = mq4_quantize_batch(jobs.data(), (int64_t)jobs.size(), group_size, bits, stream);
+    if (rc != MQ4_OK) return last_error(rc);
+    for (QuantizedTensor& q : out) q.quantized = true;
+    return out;
 }
 
 // qmatmul (src/model/marlin.cpp:18-25): y[M, N] = x[M, K] @ dequant(W)^T.

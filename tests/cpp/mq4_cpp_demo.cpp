@@ -31,17 +31,28 @@ int main(int argc, char** argv) {
     mq4::DeviceBuffer wtmp(2 * I * H > 2 * V * H ? 2 * I * H : 2 * V * H);
     std::vector<mq4::MLPWeights> layers(LAYERS);
     std::vector<mq4::DeviceBuffer> norms;
+    // the layers' bf16 weights, then one batched quantize of all of them
+    // (the loader loop of src/model/weights.cpp:147-160)
+    std::vector<mq4::DeviceBuffer> raw;
+    std::vector<mq4::WeightView> views;
     for (int l = 0; l < LAYERS; ++l) {
         const int64_t shp[3][2] = {{I, H}, {I, H}, {H, I}};
-        mq4::QuantizedTensor* dst[3] = {&layers[l].gate_proj, &layers[l].up_proj, &layers[l].down_proj};
         for (int p = 0; p < 3; ++p) {
-            if (fill(wtmp.as<uint16_t>(), shp[p][0] * shp[p][1], 1000 + 3 * l + p, 0.0, 0.02, st)) return 3;
-            auto q = mq4::quantize_weight(wtmp.as<uint16_t>(), shp[p][0], shp[p][1], st);
-            CHECK(q);
-            *dst[p] = std::move(q.value());
+            raw.emplace_back((size_t)(2 * shp[p][0] * shp[p][1]));
+            if (fill(raw.back().as<uint16_t>(), shp[p][0] * shp[p][1], 1000 + 3 * l + p, 0.0, 0.02, st)) return 3;
+            views.push_back({raw.back().as<uint16_t>(), shp[p][0], shp[p][1]});
         }
         norms.emplace_back(2 * H);
         if (fill(norms.back().as<uint16_t>(), H, 2100 + l, 0.1, 0.02, st)) return 3;
+    }
+    {
+        auto qs = mq4::quantize_weights(views, st);
+        CHECK(qs);
+        for (int l = 0; l < LAYERS; ++l) {
+            layers[l].gate_proj = std::move(qs.value()[3 * l]);
+            layers[l].up_proj = std::move(qs.value()[3 * l + 1]);
+            layers[l].down_proj = std::move(qs.value()[3 * l + 2]);
+        }
     }
     if (fill(wtmp.as<uint16_t>(), V * H, 2000, 0.0, 0.02, st)) return 3;
     auto lmq = mq4::quantize_weight(wtmp.as<uint16_t>(), V, H, st);
