@@ -610,9 +610,9 @@ def bench_pack(E, layers, lm):
     """Config 5b: quantize/pack of the full weight set (72 MLP matrices + the
     lm_head).  The bf16 weights are generated again (the same streams as the
     setup) and packed by mq4_quantize_batch (the loader's whole loop in three
-    launches of at most 32 matrices) between one pair of HIP events (median of
-    3 passes); the same 73 matrices as 73 mq4_quantize calls back to back are
-    timed beside it.  Both outputs must equal the setup's bit for bit.  The
+    launches of at most 32 matrices), 5 passes back to back between one pair
+    of HIP events (mean per pass, median of 3 such batches); the same 73
+    matrices as 73 mq4_quantize calls are timed beside it the same way.  Both outputs must equal the setup's bit for bit.  The
     setup's per-matrix timings (an event pair and a synchronize around each
     call) are reported too."""
     torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
@@ -636,7 +636,7 @@ def bench_pack(E, layers, lm):
         for (w, (N, K)), (wq, s, b) in zip(srcs, outs):
             L.mq4_quantize(P(w.data_ptr()), N, K, 64, 4, P(wq.data_ptr()), P(s.data_ptr()), P(b.data_ptr()), st)
 
-    us_sep = statistics.median([E.timed(pack_separate, 1, warm=1 if i == 0 else 0) for i in range(3)])
+    us_sep = statistics.median([E.timed(pack_separate, 5, warm=1 if i == 0 else 0) for i in range(3)])
     same_sep = same_as_setup(outs)
 
     outs_b = fresh()
@@ -648,7 +648,7 @@ def bench_pack(E, layers, lm):
     def pack_batch():
         mq4._check(L.mq4_quantize_batch(jobs_p, len(srcs), 64, 4, st))
 
-    us = statistics.median([E.timed(pack_batch, 1, warm=1 if i == 0 else 0) for i in range(3)])
+    us = statistics.median([E.timed(pack_batch, 5, warm=1 if i == 0 else 0) for i in range(3)])
     same = same_as_setup(outs_b)
     del srcs, outs, outs_b
     return {"bytes": E.pack_bytes, "us": round(us, 1), "roofline": hbm_roofline(E.pack_bytes, us),
@@ -657,8 +657,9 @@ def bench_pack(E, layers, lm):
             "separate_calls_roofline": hbm_roofline(E.pack_bytes, us_sep),
             "per_matrix_sum_us": round(E.pack_us, 1),
             "note": "read 2 B per bf16 weight + write 0.5625 B per weight (words, scales, biases); "
-                    "mq4_quantize_batch over the 73 matrices (3 launches) between one event pair, median of 3 "
-                    "passes; separate_calls_us: the same 73 matrices as 73 mq4_quantize calls back to back"}
+                    "mq4_quantize_batch over the 73 matrices (3 launches), 5 passes back to back between one "
+                    "event pair (mean per pass, median of 3); separate_calls_us: the same 73 matrices as "
+                    "73 mq4_quantize calls, timed the same way"}
 
 
 # ----------------------------------------------------------- profile modes
