@@ -38,14 +38,15 @@ __device__ __forceinline__ uint32_t code_of(float r) {
 // rounded after the second (a quotient of two floats is never a rounding
 // midpoint, so no tie can be decided the wrong way).  This holds without
 // overflow or underflow; an infinite q0 means |d / scale| > 2^127, whose
-// code is the clamp of q0 itself, and an underflowing quotient codes to 0
-// either way (|scale| >= 5e-8: the 1e-7 floor, at most halved by the edge
-// adjustment).  So rint of this quotient equals rint(d / scale) as MLX
+// code is the clamp of q0 itself (GUARD), and an underflowing quotient codes
+// to 0 either way (|scale| >= 5e-8: the 1e-7 floor, at most halved by the
+// edge adjustment).  So rint of this quotient equals rint(d / scale) as MLX
 // computes it, element by element.
+template <bool GUARD>
 __device__ __forceinline__ float quotient(float d, float scale, float inv) {
 #pragma clang fp contract(off)
     const float q0 = d * inv;
-    if (!(fabsf(q0) <= 3.4028234663852886e38f)) return q0;      // +-inf, or NaN from a NaN d
+    if (GUARD && !(fabsf(q0) <= 3.4028234663852886e38f)) return q0;   // +-inf, or NaN from a NaN d
     const float r0 = __builtin_fmaf(-q0, scale, d);
     const float q1 = __builtin_fmaf(r0, inv, q0);
     const float r1 = __builtin_fmaf(-q1, scale, d);
@@ -87,9 +88,19 @@ __device__ __forceinline__ void pack16(const uint4* v, uint32_t* word, float* sc
     }
     const float inv = 1.0f / scale;
     word[0] = word[1] = 0u;
+    // With a finite range max - min every element lies within it, so
+    // |d / scale| <= 15 (about 16 after roundings) and the quotient cannot
+    // overflow: the guard for an infinite q0 only matters for groups holding
+    // an infinity.  The choice is wave-uniform (one branch per wave).
+    if (__all(fabsf(mx - mn) <= 3.4028234663852886e38f)) {
 #pragma unroll
-    for (int p = 0; p < 16; ++p)
-        word[p >> 3] |= code_of(__builtin_rintf(quotient(f[p] - bias, scale, inv))) << (4 * (p & 7));
+        for (int p = 0; p < 16; ++p)
+            word[p >> 3] |= code_of(__builtin_rintf(quotient<false>(f[p] - bias, scale, inv))) << (4 * (p & 7));
+    } else {
+#pragma unroll
+        for (int p = 0; p < 16; ++p)
+            word[p >> 3] |= code_of(__builtin_rintf(quotient<true>(f[p] - bias, scale, inv))) << (4 * (p & 7));
+    }
     *scale_out = scale;
     *bias_out = bias;
 }

@@ -186,6 +186,64 @@ def test_quantize_batch_matches_oracle(mq4, O, dev):
         assert torch.equal(sq, wq) and torch.equal(ss, s) and torch.equal(sb, b), i
 
 
+def test_quantize_non_finite_groups(mq4, O, dev):
+    """Groups holding +-inf, NaN (some or all elements) or extremes whose range
+    overflows float32 (+-3e38): the kernel's guarded quotient path (any group
+    with a non-finite range in the wave) must give the oracle's codes, scales
+    and biases, and the finite groups of the same waves theirs."""
+    rng = np.random.default_rng(13)
+    groups = []
+    specials = [np.inf, -np.inf, np.nan]
+    for gi in range(256):
+        v = (rng.standard_normal(64) * 0.02).astype(np.float32)
+        kind = gi % 8
+        if kind == 0:
+            v[rng.integers(0, 64)] = specials[gi // 8 % 3]
+        elif kind == 1:
+            v[rng.integers(0, 64, 5)] = np.nan
+        elif kind == 2:
+            v[:] = np.nan
+        elif kind == 3:
+            v[0], v[1] = 3.0e38, -3.0e38
+        groups.append(O.f32_to_bf16(v))
+    wh = np.stack(groups).reshape(64, 256)
+    print("quantize non-finite groups", flush=True)
+    wq, s, b = mq4.quantize(to_dev_bf16(wh, dev))
+    torch.cuda.synchronize()
+    rq, rs, rb = O.quantize(wh)
+    assert np.array_equal(to_host_u16(s), rs)
+    assert np.array_equal(to_host_u16(b), rb)
+    assert np.array_equal(words(wq), rq)
+
+
+def test_quantize_word_output_only_4_byte_aligned(mq4, O, dev):
+    """wq needs only 4-byte alignment (the kernels store 4-byte words): a wq
+    4 bytes past an 8-byte boundary gets the oracle's words, single and
+    batched, and nothing is written outside it."""
+    import ctypes
+    N, K = 96, 640
+    w, wh = gen_weight(mq4, O, 3100, N, K)
+    rq, rs, rb = O.quantize(wh)
+    L = mq4.lib()
+    store = torch.zeros(N * K // 8 + 2, dtype=torch.int32, device=dev)
+    wq = store[1:1 + N * K // 8]                     # 4 bytes past an 8-byte boundary
+    assert wq.data_ptr() % 8 == 4
+    s = torch.empty((N, K // 64), dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(s)
+    print("quantize into a 4-byte-aligned wq", flush=True)
+    assert L.mq4_quantize(w.data_ptr(), N, K, 64, 4, wq.data_ptr(), s.data_ptr(), b.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(wq.cpu().numpy().view(np.uint32).reshape(N, K // 8), rq)
+    assert np.array_equal(to_host_u16(s), rs) and np.array_equal(to_host_u16(b), rb)
+    store.zero_()
+    jobs = (mq4._QuantJobC * 2)(mq4._QuantJobC(w.data_ptr(), N, K, wq.data_ptr(), s.data_ptr(), b.data_ptr()),
+                                mq4._QuantJobC(w.data_ptr(), N, K, wq.data_ptr(), s.data_ptr(), b.data_ptr()))
+    assert L.mq4_quantize_batch(ctypes.cast(jobs, ctypes.c_void_p), 1, 64, 4, None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(wq.cpu().numpy().view(np.uint32).reshape(N, K // 8), rq)
+    assert int(store[0].item()) == 0 and int(store[-1].item()) == 0      # nothing written outside wq
+
+
 def test_dequantize_matches_affine_formula(mq4, O, dev):
     N, K = 96, 2048
     w, wh = gen_weight(mq4, O, 9, N, K)
