@@ -78,6 +78,8 @@ def parse():
                    help="eager steps with per-kernel HIP events (separate kernels)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-configs", action="store_true", help="headline only")
+    p.add_argument("--only", default=None,
+                   help="comma-separated config names to run (e.g. config5a_batched); default all")
     p.add_argument("--cpu-reps", type=int, default=3)
     p.add_argument("--profile-kernel", default=None,
                    choices=["decode_step", "copy", "gemv_gate", "lm_head", "prefill", "batched", "pack"],
@@ -369,6 +371,8 @@ def main():
                          ("config5b_pack", lambda: bench_pack(E, layers, lm)),
                          ("next_q4_projections", lambda: bench_projections(E, x0)),
                          ("next_sampling", lambda: bench_sampling(E, lm, norm_w, x0))):
+            if args.only and name not in args.only.split(","):
+                continue
             try:
                 configs[name] = fn()
                 log(f"[bench] {name}: {json.dumps(configs[name])}")
