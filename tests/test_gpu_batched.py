@@ -11,7 +11,10 @@ shapes through the C ABI, against the oracle on the same seeded inputs:
 * lm_head + greedy argmax over the full 248,320-row vocab
   (src/model/marlin.cpp:161-169, src/sampling/sampler.cpp:14-16): logits
   >= 98% identical to bf16(fp64), indices bit-exact on the kernel's own
-  logits and equal to the fp64 argmax unless the top two are within 1 ulp.
+  logits and equal to the fp64 argmax unless the top two are within 1 ulp;
+* edge shapes (test_batched_edge_shapes): odd M on either side of the
+  16-row tile, ragged N, K of 1024 to 6144, every epilogue, and a store
+  with more tiles than resident workgroups.
 """
 import numpy as np
 import pytest
@@ -127,3 +130,58 @@ def test_batched_qmm_f32_bar(mq4, O, dev, mlp, M):
     err = rel_err_f32(y32.cpu().numpy(), ref)
     print(f"gate fp32 M={M}: max|err|/rms = {err:.2e}")
     assert err <= 1e-4
+
+
+# (M, N, K, what): odd M on either side of the 16-row tile, ragged N, K beyond
+# the model's 2048 (other wave layouts, activations re-read per group at
+# M > 16 and K > 2048), and a store with more 16-row tiles (750) than
+# resident workgroups, so that workgroups loop over rounds with the next
+# round's weights in flight.
+EDGE = [(5, 200, 1024, "store"), (9, 1000, 2048, "f32"), (17, 520, 4096, "residual"),
+        (31, 12000, 1024, "store"), (12, 6144, 1024, "swiglu"), (23, 1000, 2048, "argmax"),
+        (7, 3000, 2048, "norm_swiglu"), (20, 256, 6144, "f32"), (29, 1000, 2048, "norm_swiglu")]
+
+
+@pytest.mark.parametrize("case", EDGE, ids=lambda c: "-".join(map(str, c)))
+def test_batched_edge_shapes(mq4, O, dev, case):
+    M, N, K, what = case
+    print(f"batched edge M={M} N={N} K={K} {what}", flush=True)
+    sid = 5000 + EDGE.index(case)
+    w = mq4.quantize_weight(mq4.fill_normal_bf16((N, K), sid, 0.0, 0.02, device=dev))
+    wh = q_host(w)
+    xh = O.gen_normal_bf16(sid + 100, M * K, 0.0, 1.0).reshape(M, K)
+    x = to_dev_bf16(xh, dev)
+    if what in ("store", "f32"):
+        y = mq4.qmatmul(x, w)
+        y32 = mq4.quantized_matmul_f32(x, w.weight, w.scales, w.biases)
+        torch.cuda.synchronize()
+        y64, _ = O.qmm_f64(xh, *wh)
+        check_close(O, to_host_u16(y), y64, f"edge {case}", y32.cpu().numpy())
+        assert rel_err_f32(y32.cpu().numpy(), y64) <= 1e-4
+    elif what == "residual":
+        rh = O.gen_normal_bf16(sid + 200, M * N).reshape(M, N)
+        y = mq4.qmatmul_residual(x, w, to_dev_bf16(rh, dev))
+        yq = mq4.qmatmul(x, w)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host_u16(y), O.add_bf16(rh, to_host_u16(yq)))
+        y64, _ = O.qmm_f64(xh, *wh)
+        check_close(O, to_host_u16(yq), y64, f"edge {case}")
+    elif what in ("swiglu", "norm_swiglu"):
+        u = mq4.quantize_weight(mq4.fill_normal_bf16((N, K), sid + 300, 0.0, 0.02, device=dev))
+        uh = q_host(u)
+        nwh = O.gen_normal_bf16(sid + 400, K, 0.1, 0.02)
+        norm = what == "norm_swiglu"
+        h = mq4.mlp_gate_up_silu(x, w, u, norm_weight=to_dev_bf16(nwh, dev) if norm else None, eps=1e-6)
+        torch.cuda.synchronize()
+        n = O.rmsnorm_1pw(xh, nwh, 1e-6) if norm else xh
+        _, gb = O.qmm_f64(n, *wh)
+        _, ub = O.qmm_f64(n, *uh)
+        check_swiglu(O, to_host_u16(h), O.swiglu_bf16(gb, ub), f"edge {case}")
+    else:
+        idx, logits = mq4.lm_head_argmax(x, w, return_logits=True)
+        torch.cuda.synchronize()
+        lg = to_host_u16(logits)
+        got = idx.cpu().numpy().astype(np.uint32)
+        assert np.array_equal(got, O.argmax_bf16(lg))
+        y64, yb = O.qmm_f64(xh, *wh)
+        check_close(O, lg, y64, f"edge {case}")
