@@ -485,20 +485,22 @@ __device__ __forceinline__ void for_chunk(const uint16_t* __restrict__ row, int6
 }
 
 // Thread t (< 256) sums bin t over the P partial histograms part[P][256]
-// into lds[t]; the caller synchronises before reading lds.
+// into lds[t]; the caller synchronises before reading lds.  The sums are
+// integers (counts, fixed-point masses), so the order does not matter: 64
+// loads per batch are issued before any is added (clamped addresses, the
+// ones past P added as 0), so P <= 128 chunks cost two round trips to L2.
 template <class T>
 __device__ __forceinline__ T reduce_bins(const T* __restrict__ part, int P, T* lds) {
+    constexpr int kBatch = 64;
     T s = 0;
     const T* p = part + threadIdx.x;
-    int q = 0;
-    for (; q + 16 <= P; q += 16) {                 // sixteen independent loads in flight
-        T v[16];
+    for (int q = 0; q < P; q += kBatch) {
+        T v[kBatch];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = p[(size_t)(q + j) * 256];
+        for (int j = 0; j < kBatch; ++j) v[j] = p[(size_t)(q + j < P ? q + j : P - 1) * 256];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s += v[j];
+        for (int j = 0; j < kBatch; ++j) s += q + j < P ? v[j] : (T)0;
     }
-    for (; q < P; ++q) s += p[(size_t)q * 256];
     lds[threadIdx.x] = s;
     return s;
 }
