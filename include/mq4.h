@@ -152,7 +152,10 @@ int mq4_mlp_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
  * math, one rounding), h = swiglu(xn @ Wg^T, xn @ Wu^T).  Replaces
  * rms_norm(hidden, post_attn_norm) + mlp_forward's gate/up/swiglu
  * (src/model/marlin.cpp:141, 12-16, 27-33).  norm_weight is bf16 [K],
- * 16-byte aligned. */
+ * 16-byte aligned.  From M = 33 rows on, mq4_rms_norm into a [M, K] buffer
+ * followed by mq4_mlp_gate_up_silu gives the same normalized operand and
+ * takes about half the time (this fused form normalizes every activation
+ * tile in registers before staging it). */
 int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
                              const uint16_t* norm_weight, float eps,
                              const uint32_t* gate_wq, const uint16_t* gate_scales,

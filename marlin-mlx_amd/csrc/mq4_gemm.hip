@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm_kernel(GemmArgs p) {
 
 // ---------------------------------------------------------------------------
 // The same product with every operand staged by LDS DMA (global_load_lds)
-// through a 3-stage ring, for the epilogues without the fused norm.  A block
+// through a ring of S = 2 (or 3) stages, for the epilogues without the fused norm.  A block
 // is WM x WN waves of 64 rows x 64 weight columns each (BM = 64 WM rows,
 // BNW = 64 WN weight columns):
 //  * per group, BM x 64 activations (each row's eight 16-byte chunks
@@ -343,7 +343,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr uint32_t kPermLo = 0x05040100u, kPermHi = 0x07060302u;
 
 template <int EPI, int WM, int WN, int S>
-__global__ __launch_bounds__(64 * WM * WN, 1) void q4_gemm_dma_kernel(GemmArgs p) {
+__global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p) {
 #pragma clang fp contract(off)
     constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
     constexpr int NW = WM * WN;
@@ -360,7 +360,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q4_gemm_dma_kernel(GemmArgs p
     __shared__ St st0, st1;
     __shared__ St2 st2;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // the wave index is uniform: kept in scalar registers, as is everything
+    // derived from it below (DMA bases and LDS destinations)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int h = lane >> 5, col = lane & 31;
     const int M = p.M, N = p.N, K = p.K, G = K / 64;
@@ -380,43 +383,52 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void q4_gemm_dma_kernel(GemmArgs p
     }
     const int n0 = nb * BN, m0 = mb * TBM;
 
-    // ---- DMA sources of this lane (group g adds g * 64 elements along K) ----
-    const uint16_t* asrc[A_I];
+    // ---- DMA sources: per instruction a wave-uniform base (scalar
+    // registers; group g moves it along K) plus a 32-bit byte offset per
+    // lane (the host takes this kernel only when every offset fits) ----
+    const char* const xbase = reinterpret_cast<const char*>(p.x);
+    uint32_t aoff[A_I];
 #pragma unroll
     for (int t = 0; t < A_I; ++t) {
         const int slot = (wave * A_I + t) * 64 + lane;
         const int r = slot >> 3, c = (slot & 7) ^ ((r >> 1) & 7);
         const int row = (m0 + r) < M ? (m0 + r) : (M - 1);
-        asrc[t] = p.x + (int64_t)row * K + c * 8;
+        aoff[t] = (uint32_t)(((int64_t)row * K + c * 8) * 2);
     }
-    // weight row r of the block -> matrix and output row
+    // weight row r of the block -> matrix and output row; the 64 slots of
+    // one DMA instruction lie in one matrix and one k-half
+    static_assert(NMAT == 1 || (BNW / 2) % 64 == 0, "one matrix per DMA instruction");
     auto wrow_of = [&](int r) -> int {
         const int n = NMAT == 2 ? n0 + (r % (BNW / 2)) : n0 + r;
         return n < N ? n : N - 1;
     };
     auto mat_of = [&](int r) -> const QMat& { return (NMAT == 2 && r >= BNW / 2) ? p.B : p.A; };
-    const uint32_t* bsrc[B_I];
+    const char* bbase[B_I];
+    uint32_t boff[B_I];
 #pragma unroll
     for (int t = 0; t < B_I; ++t) {
-        const int q = (wave * B_I + t) * 64 + lane, half = q / BNW, r = q % BNW;
-        bsrc[t] = mat_of(r).wq + (int64_t)wrow_of(r) * (K / 8) + half * 4;
+        const int q0 = (wave * B_I + t) * 64, half = q0 / BNW, r0 = q0 % BNW;
+        bbase[t] = reinterpret_cast<const char*>(mat_of(r0).wq) + half * 16;
+        boff[t] = (uint32_t)((int64_t)wrow_of(r0 + lane) * (K / 2));
     }
-    const uint16_t* sbsrc[SB_I];
+    const char* sbbase[SB_I];
+    uint32_t sboff[SB_I];
 #pragma unroll
     for (int t = 0; t < SB_I; ++t) {
-        const int u = (wave * SB_I + t) * 64 + lane, sel = u / BNW, r = u % BNW;
-        sbsrc[t] = (sel ? mat_of(r).b : mat_of(r).s) + (int64_t)wrow_of(r) * G;
+        const int u0 = (wave * SB_I + t) * 64, sel = u0 / BNW, r0 = u0 % BNW;
+        sbbase[t] = reinterpret_cast<const char*>(sel ? mat_of(r0).b : mat_of(r0).s);
+        sboff[t] = (uint32_t)((int64_t)wrow_of(r0 + lane) * G * 2);
     }
     auto issue = [&](int g, St& st) {
 #pragma unroll
         for (int t = 0; t < A_I; ++t)
-            lds_dma16(asrc[t] + g * 64, &st.a[(wave * A_I + t) * 64]);
+            lds_dma16(xbase + g * 128 + aoff[t], &st.a[(wave * A_I + t) * 64]);
 #pragma unroll
         for (int t = 0; t < B_I; ++t)
-            lds_dma16(bsrc[t] + g * 8, &st.b[(wave * B_I + t) * 64]);
+            lds_dma16(bbase[t] + g * 32 + boff[t], &st.b[(wave * B_I + t) * 64]);
 #pragma unroll
         for (int t = 0; t < SB_I; ++t)
-            lds_dma4(sbsrc[t] + (g & ~1), &st.sb[0][(wave * SB_I + t) * 64]);
+            lds_dma4(sbbase[t] + (g & ~1) * 2 + sboff[t], &st.sb[0][(wave * SB_I + t) * 64]);
     };
 
     // ---- compute roles: weight row of tile j for this lane ----
@@ -577,9 +589,9 @@ void launch_dma(const GemmArgs& a, hipStream_t st) {
 }
 
 // The layout used for every shape: 2 x 2 waves, 2 stages.  Measured on
-// MI355X at M = 2048 / 8192 against 1 x 2, 1 x 4 and 2 x 2 with 3 stages it
-// is as fast or faster for both the gate/up (N = 6144) and the down
-// (N = 2048) products, with the least LDS (41 KB, so two blocks per CU).
+// MI355X at M = 1960 / 2048 / 8192 against 1 x 2, 1 x 4 and 2 x 2 with 3
+// stages it is as fast or faster for both the gate/up (N = 6144) and the
+// down (N = 2048) products, with the least LDS (41 KB, so two blocks per CU).
 template <int EPI>
 void launch_dma_auto(const GemmArgs& a, hipStream_t st) {
     launch_dma<EPI, 2, 2, 2>(a, st);
@@ -591,7 +603,9 @@ template <int EPI, bool NORM>
 void launch(const GemmArgs& a, hipStream_t st) {
     constexpr int BN = EPI == GEMM_SWIGLU ? 64 : 128;
     const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM));
-    const bool dma_ok = ((a.K / 64) % 2 == 0) && reinterpret_cast<uintptr_t>(a.A.s) % 4 == 0 &&
+    // the DMA kernel addresses x and the weights by 32-bit byte offsets
+    const bool fits32 = (int64_t)a.M * a.K * 2 <= 0xFFFFFFFFLL && (int64_t)a.N * a.K / 2 <= 0xFFFFFFFFLL;
+    const bool dma_ok = fits32 && ((a.K / 64) % 2 == 0) && reinterpret_cast<uintptr_t>(a.A.s) % 4 == 0 &&
                         reinterpret_cast<uintptr_t>(a.A.b) % 4 == 0 &&
                         (EPI != GEMM_SWIGLU ||
                          (reinterpret_cast<uintptr_t>(a.B.s) % 4 == 0 && reinterpret_cast<uintptr_t>(a.B.b) % 4 == 0));
