@@ -12,9 +12,9 @@
 // row-major [N, K] matrix are consecutive 64-element (128-byte) runs, and the
 // packed words, scales and biases of group g sit at wq[8g..8g+7], scales[g],
 // biases[g].  So the whole matrix is one flat stream of groups and the kernel
-// never needs N or K: each lane reads 32 bytes (16 bf16) and writes two packed
-// words per step, four lanes form a group, and a wave covers 16 groups =
-// 2 KiB of input per step with coalesced 16-byte loads and word stores.
+// never needs N or K: four lanes share a group, each reading 32 bytes
+// (16 bf16) and writing two packed words per step, and a wave covers 16
+// groups = 2 KiB of input per step with coalesced 16-byte loads.
 #include "mq4_device.h"
 #include "mq4_host.h"
 
@@ -22,13 +22,6 @@ namespace mq4 {
 
 __device__ __forceinline__ float mlx_max(float a, float b) { return (a < b) ? b : a; }
 __device__ __forceinline__ float mlx_min(float a, float b) { return (b < a) ? b : a; }
-
-// Code of one element: clamp(rint(x), 0, 15) with NaN -> 0, where x is the
-// quotient (w - bias) / scale.  fmaxf/fminf give the same code as MLX's
-// max/min-then-NaN-check (a NaN quotient lands on 0 either way).
-__device__ __forceinline__ uint32_t code_of(float r) {
-    return (uint32_t)fminf(fmaxf(r, 0.0f), 15.0f);
-}
 
 // The correctly rounded quotient d / scale without a division: inv =
 // RN(1 / scale) is the correctly rounded reciprocal, q0 = RN(d * inv) is
@@ -53,12 +46,46 @@ __device__ __forceinline__ float quotient(float d, float scale, float inv) {
     return __builtin_fmaf(r1, inv, q1);
 }
 
-// One group step over 16 values per lane (four lanes form a group).
-__device__ __forceinline__ void pack16(const uint4* v, uint32_t* word, float* scale_out, float* bias_out) {
+// The packed words of V consecutive weights f of a group.  The code of each
+// weight, clamp(rint(x), 0, 15) of its quotient x = (f - bias) / scale with
+// NaN -> 0 (fmaxf/fminf give the same code as MLX's max/min-then-NaN-check),
+// lands in the low byte of t: the clamp comes first (to integer bounds, so
+// the order does not matter), then rint by adding 1.5 * 2^23, whose float
+// sum has unit spacing and rounds half to even, leaving the integer in the
+// low mantissa bits (0x4B40000k).  Byte b of word i is then
+// (code 8i+2b+1) << 4 | code 8i+2b, gathered by two byte permutes.
+template <bool GUARD, int V>
+__device__ __forceinline__ void pack_words(const float (&f)[V], float bias, float scale, float inv,
+                                           uint32_t (&word)[V / 8]) {
 #pragma clang fp contract(off)
-    float f[16];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
+    for (int i = 0; i < V / 8; ++i) {
+        uint32_t t[8];
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+            t[p] = __builtin_bit_cast(
+                uint32_t, fminf(fmaxf(quotient<GUARD>(f[8 * i + p] - bias, scale, inv), 0.0f), 15.0f) + 12582912.0f);
+        uint32_t u[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) u[b] = (t[2 * b + 1] << 4) | t[2 * b];
+        const uint32_t lo = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0400u);
+        word[i] = lo | (hi << 16);
+    }
+}
+
+// LPG lanes (consecutive, all active or all inactive) share a group of 64
+// weights, V = 64 / LPG each (v: the lane's V / 8 consecutive 16-byte
+// chunks) -> the lane's packed words, and the group's scale and bias (the
+// same in every lane of the group).
+template <int LPG>
+__device__ __forceinline__ void pack_group(const uint4 (&v)[8 / LPG], uint32_t (&word)[8 / LPG],
+                                           float& scale_out, float& bias_out) {
+#pragma clang fp contract(off)
+    constexpr int V = 64 / LPG;
+    float f[V];
+#pragma unroll
+    for (int k = 0; k < V / 8; ++k) {
         f[8 * k + 0] = bf16_to_f32(v[k].x & 0xffffu); f[8 * k + 1] = bf16_to_f32(v[k].x >> 16);
         f[8 * k + 2] = bf16_to_f32(v[k].y & 0xffffu); f[8 * k + 3] = bf16_to_f32(v[k].y >> 16);
         f[8 * k + 4] = bf16_to_f32(v[k].z & 0xffffu); f[8 * k + 5] = bf16_to_f32(v[k].z >> 16);
@@ -68,9 +95,9 @@ __device__ __forceinline__ void pack16(const uint4* v, uint32_t* word, float* sc
     // std::max/std::min scan from -inf/+inf.
     float mx = -__builtin_inff(), mn = __builtin_inff();
 #pragma unroll
-    for (int p = 0; p < 16; ++p) { mx = fmaxf(mx, f[p]); mn = fminf(mn, f[p]); }
+    for (int p = 0; p < V; ++p) { mx = fmaxf(mx, f[p]); mn = fminf(mn, f[p]); }
 #pragma unroll
-    for (int m = 1; m < 4; m <<= 1) {
+    for (int m = 1; m < LPG; m <<= 1) {
         mx = fmaxf(mx, __shfl_xor(mx, m));
         mn = fminf(mn, __shfl_xor(mn, m));
     }
@@ -87,67 +114,72 @@ __device__ __forceinline__ void pack16(const uint4* v, uint32_t* word, float* sc
         bias = edge;
     }
     const float inv = 1.0f / scale;
-    word[0] = word[1] = 0u;
     // With a finite range max - min every element lies within it, so
     // |d / scale| <= 15 (about 16 after roundings) and the quotient cannot
     // overflow: the guard for an infinite q0 only matters for groups holding
     // an infinity.  The choice is wave-uniform (one branch per wave).
-    if (__all(fabsf(mx - mn) <= 3.4028234663852886e38f)) {
-#pragma unroll
-        for (int p = 0; p < 16; ++p)
-            word[p >> 3] |= code_of(__builtin_rintf(quotient<false>(f[p] - bias, scale, inv))) << (4 * (p & 7));
-    } else {
-#pragma unroll
-        for (int p = 0; p < 16; ++p)
-            word[p >> 3] |= code_of(__builtin_rintf(quotient<true>(f[p] - bias, scale, inv))) << (4 * (p & 7));
-    }
-    *scale_out = scale;
-    *bias_out = bias;
+    if (__all(fabsf(mx - mn) <= 3.4028234663852886e38f))
+        pack_words<false, V>(f, bias, scale, inv, word);
+    else
+        pack_words<true, V>(f, bias, scale, inv, word);
+    scale_out = scale;
+    bias_out = bias;
 }
 
-// Grid-stride pass over one flat stream of n_pairs word pairs: each lane
-// packs two consecutive words (16 weights) per step and takes two steps per
-// loop iteration, with all four 16-byte loads issued first.
-__device__ __forceinline__ void quantize_stream(const uint4* __restrict__ w, int64_t n_pairs,
+// Grid-stride pass over one flat stream of n_groups groups, LPG lanes per
+// group and step, the next step's loads issued before this step's
+// arithmetic.  Packed words go out as 16-byte stores when wq is 16-byte
+// aligned, else as word stores.  Four lanes per group (16 weights, 66
+// VGPRs, 7 waves per SIMD) measured fastest on MI355X; with two or one
+// lane(s) per group the group's divisions are shared by fewer weights, but
+// the 32 or 64 values held per lane cut the resident waves to 4 or 2 and
+// the whole weight set took 1045 / 1548 us instead of 844 us.
+constexpr int kQuantLanesPerGroup = 4;
+__device__ __forceinline__ void quantize_stream(const uint4* __restrict__ w, int64_t n_groups,
                                                 uint32_t* __restrict__ wq, uint16_t* __restrict__ scales,
                                                 uint16_t* __restrict__ biases) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    // The loop bound is block-uniform so the cross-lane reductions run with
-    // every lane of the wave active.
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < n_pairs; base += 2 * stride) {
-        int64_t idx[2];
-        bool live[2];
-        uint4 v[2][2];
+    constexpr int LPG = kQuantLanesPerGroup, NC = 8 / LPG;      // 16-byte chunks per lane
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x / LPG;
+    const bool wide = (reinterpret_cast<uintptr_t>(wq) & 15) == 0;
+    const int part = threadIdx.x % LPG;
+    int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPG;
+    uint4 nxt[NC];
+    if (g < n_groups) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            idx[u] = base + u * stride + threadIdx.x;
-            live[u] = idx[u] < n_pairs;          // uniform within each 4-lane group
-            v[u][0] = live[u] ? load_nt_u4(w + 2 * idx[u]) : make_uint4(0u, 0u, 0u, 0u);
-            v[u][1] = live[u] ? load_nt_u4(w + 2 * idx[u] + 1) : make_uint4(0u, 0u, 0u, 0u);
+        for (int c = 0; c < NC; ++c) nxt[c] = load_nt_u4(w + 8 * g + NC * part + c);
+    }
+    for (; g < n_groups; g += stride) {
+        uint4 cur[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) cur[c] = nxt[c];
+        if (g + stride < n_groups) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) nxt[c] = load_nt_u4(w + 8 * (g + stride) + NC * part + c);
         }
+        uint32_t word[NC];
+        float scale, bias;
+        pack_group<LPG>(cur, word, scale, bias);
+        uint32_t* dst = wq + 8 * g + NC * part;
+        if (NC % 4 == 0 && wide) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            uint32_t word[2];
-            float scale, bias;
-            pack16(v[u], word, &scale, &bias);
-            if (live[u]) {
-                const int64_t i = idx[u];
-                wq[2 * i] = word[0];
-                wq[2 * i + 1] = word[1];
-                if ((threadIdx.x & 3) == 0) {
-                    scales[i >> 2] = (uint16_t)f32_to_bf16(scale);
-                    biases[i >> 2] = (uint16_t)f32_to_bf16(bias);
-                }
-            }
+            for (int c = 0; c < NC; c += 4)
+                *reinterpret_cast<uint4*>(dst + c) = make_uint4(word[c], word[c + 1], word[c + 2], word[c + 3]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) dst[c] = word[c];
+        }
+        if (part == 0) {
+            scales[g] = (uint16_t)f32_to_bf16(scale);
+            biases[g] = (uint16_t)f32_to_bf16(bias);
         }
     }
 }
 
-__global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w, int64_t n_words,
+__global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w, int64_t n_groups,
                                                            uint32_t* __restrict__ wq,
                                                            uint16_t* __restrict__ scales,
                                                            uint16_t* __restrict__ biases) {
-    quantize_stream(w, n_words >> 1, wq, scales, biases);
+    quantize_stream(w, n_groups, wq, scales, biases);
 }
 
 // Several matrices in one launch: the jobs' flat streams one after the other
@@ -160,12 +192,12 @@ struct QuantBatch {
     uint32_t* wq[kQuantBatch];
     uint16_t* s[kQuantBatch];
     uint16_t* b[kQuantBatch];
-    int64_t n_pairs[kQuantBatch];
+    int64_t n_groups[kQuantBatch];
     int n;
 };
 
 __global__ __launch_bounds__(256) void quantize_g64_batch_kernel(QuantBatch a) {
-    for (int j = 0; j < a.n; ++j) quantize_stream(a.w[j], a.n_pairs[j], a.wq[j], a.s[j], a.b[j]);
+    for (int j = 0; j < a.n; ++j) quantize_stream(a.w[j], a.n_groups[j], a.wq[j], a.s[j], a.b[j]);
 }
 
 // One packed word per lane: 8 outputs = scale * q + bias (q * scale is exact
@@ -267,11 +299,11 @@ extern "C" int mq4_quantize(const uint16_t* w, int64_t N, int64_t K, int group_s
     if (!aligned(w, 16) || !aligned(wq, 4) || !aligned(scales, 2) || !aligned(biases, 2))
         return fail(MQ4_ERR_ALIGNMENT, "%s: w must be 16-byte aligned, wq 4-byte, scales/biases 2-byte",
                     what);
-    const int64_t n_words = N * (K / 8);    // a multiple of 8: whole groups, whole word pairs
+    const int64_t n_groups = N * (K / 64);
     const int block = 256;
-    const int grid = grid_for((n_words / 2 + 1) / 2, block, 256 * 32);
+    const int grid = grid_for(n_groups * kQuantLanesPerGroup, block, 256 * 32);
     hipLaunchKernelGGL(quantize_g64_kernel, dim3(grid), dim3(block), 0, as_stream(stream),
-                       reinterpret_cast<const uint4*>(w), n_words, wq, scales, biases);
+                       reinterpret_cast<const uint4*>(w), n_groups, wq, scales, biases);
     return launch_status(what);
 }
 
@@ -305,12 +337,12 @@ extern "C" int mq4_quantize_batch(const mq4_quantize_job* jobs, int64_t n_jobs, 
             a.wq[i] = q.wq;
             a.s[i] = q.scales;
             a.b[i] = q.biases;
-            a.n_pairs[i] = q.N * (q.K / 16);
+            a.n_groups[i] = q.N * (q.K / 64);
         }
         // enough lanes to keep HBM busy, not more than the largest job uses
         int64_t largest = 0;
-        for (int i = 0; i < a.n; ++i) largest = a.n_pairs[i] > largest ? a.n_pairs[i] : largest;
-        const int grid = grid_for((largest + 1) / 2, 256, 256 * 32);
+        for (int i = 0; i < a.n; ++i) largest = a.n_groups[i] > largest ? a.n_groups[i] : largest;
+        const int grid = grid_for(largest * kQuantLanesPerGroup, 256, 256 * 32);
         hipLaunchKernelGGL(quantize_g64_batch_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a);
         if (int rc = launch_status(what)) return rc;
     }
