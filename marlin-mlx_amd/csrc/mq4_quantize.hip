@@ -46,6 +46,17 @@ __device__ __forceinline__ float quotient(float d, float scale, float inv) {
     return __builtin_fmaf(r1, inv, q1);
 }
 
+// x / 15 correctly rounded for finite x >= 0, without a division: one
+// Markstein step q + RN(x - 15 q) * y from q = RN(x * y), y = RN(1 / 15).
+// Checked against IEEE x / 15 for every non-negative finite float
+// (subnormals and zero included), with no mismatch.
+__device__ __forceinline__ float div15(float x) {
+#pragma clang fp contract(off)
+    const float y = 0x1.111112p-4f;
+    const float q = x * y;
+    return __builtin_fmaf(__builtin_fmaf(-q, 15.0f, x), y, q);
+}
+
 // The packed words of V consecutive weights f of a group.  The code of each
 // weight, clamp(rint(x), 0, 15) of its quotient x = (f - bias) / scale with
 // NaN -> 0 (fmaxf/fminf give the same code as MLX's max/min-then-NaN-check),
@@ -103,7 +114,17 @@ __device__ __forceinline__ void pack_group(const uint4 (&v)[8 / LPG], uint32_t (
     }
     const float n_bins = 15.0f;
     const float eps = 1e-7f;
-    float scale = mlx_max((mx - mn) / n_bins, eps);
+    // With a finite range max - min every element lies within it, so
+    // |d / scale| <= 15 (about 16 after roundings) and no quotient below can
+    // overflow; the guards only matter for groups holding an infinity or
+    // only NaNs.  The choice is wave-uniform (one branch per wave).
+    const float range = mx - mn;
+    const bool finite = __all(fabsf(range) <= 3.4028234663852886e38f);
+    float scale;
+    if (finite)
+        scale = mlx_max(div15(range), eps);
+    else
+        scale = mlx_max(range / n_bins, eps);
     const bool side = fabsf(mn) > fabsf(mx);
     scale = side ? scale : -scale;
     const float edge = side ? mn : mx;
@@ -114,11 +135,7 @@ __device__ __forceinline__ void pack_group(const uint4 (&v)[8 / LPG], uint32_t (
         bias = edge;
     }
     const float inv = 1.0f / scale;
-    // With a finite range max - min every element lies within it, so
-    // |d / scale| <= 15 (about 16 after roundings) and the quotient cannot
-    // overflow: the guard for an infinite q0 only matters for groups holding
-    // an infinity.  The choice is wave-uniform (one branch per wave).
-    if (__all(fabsf(mx - mn) <= 3.4028234663852886e38f))
+    if (finite)
         pack_words<false, V>(f, bias, scale, inv, word);
     else
         pack_words<true, V>(f, bias, scale, inv, word);
