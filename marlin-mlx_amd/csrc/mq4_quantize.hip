@@ -150,49 +150,58 @@ __device__ __forceinline__ void pack_group(const uint4 (&v)[8 / LPG], uint32_t (
 // VGPRs, 7 waves per SIMD) measured fastest on MI355X; with two or one
 // lane(s) per group the group's divisions are shared by fewer weights, but
 // the 32 or 64 values held per lane cut the resident waves to 4 or 2 and
-// the whole weight set took 1045 / 1548 us instead of 844 us.
+// the whole weight set took 1045 / 1548 us instead of 844 us.  Addresses
+// are 32-bit byte offsets from the (scalar) base pointers, so a stream
+// holds fewer than kQuantMaxGroups groups (the host splits longer ones).
 constexpr int kQuantLanesPerGroup = 4;
-__device__ __forceinline__ void quantize_stream(const uint4* __restrict__ w, int64_t n_groups,
+constexpr int64_t kQuantMaxGroups = int64_t(1) << 25;       // 2^25 groups x 128 B = 4 GiB of input
+__device__ __forceinline__ void quantize_stream(const uint4* __restrict__ w, uint32_t n_groups,
                                                 uint32_t* __restrict__ wq, uint16_t* __restrict__ scales,
                                                 uint16_t* __restrict__ biases) {
     constexpr int LPG = kQuantLanesPerGroup, NC = 8 / LPG;      // 16-byte chunks per lane
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x / LPG;
+    const uint32_t stride = gridDim.x * blockDim.x / LPG;
     const bool wide = (reinterpret_cast<uintptr_t>(wq) & 15) == 0;
-    const int part = threadIdx.x % LPG;
-    int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPG;
+    const uint32_t part = threadIdx.x % LPG;
+    const char* const wb = reinterpret_cast<const char*>(w);
+    char* const qb = reinterpret_cast<char*>(wq);
+    char* const sb = reinterpret_cast<char*>(scales);
+    char* const bb = reinterpret_cast<char*>(biases);
+    uint32_t g = (blockIdx.x * blockDim.x + threadIdx.x) / LPG;
     uint4 nxt[NC];
     if (g < n_groups) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) nxt[c] = load_nt_u4(w + 8 * g + NC * part + c);
+        for (int c = 0; c < NC; ++c) nxt[c] = load_nt_u4(reinterpret_cast<const uint4*>(wb + (g * 128u + part * (16u * NC) + c * 16u)));
     }
     for (; g < n_groups; g += stride) {
         uint4 cur[NC];
 #pragma unroll
         for (int c = 0; c < NC; ++c) cur[c] = nxt[c];
-        if (g + stride < n_groups) {
+        const uint32_t gn = g + stride;
+        if (gn < n_groups) {
 #pragma unroll
-            for (int c = 0; c < NC; ++c) nxt[c] = load_nt_u4(w + 8 * (g + stride) + NC * part + c);
+            for (int c = 0; c < NC; ++c)
+                nxt[c] = load_nt_u4(reinterpret_cast<const uint4*>(wb + (gn * 128u + part * (16u * NC) + c * 16u)));
         }
         uint32_t word[NC];
         float scale, bias;
         pack_group<LPG>(cur, word, scale, bias);
-        uint32_t* dst = wq + 8 * g + NC * part;
+        const uint32_t wo = g * 32u + part * (4u * NC);
         if (NC % 4 == 0 && wide) {
 #pragma unroll
             for (int c = 0; c < NC; c += 4)
-                *reinterpret_cast<uint4*>(dst + c) = make_uint4(word[c], word[c + 1], word[c + 2], word[c + 3]);
+                *reinterpret_cast<uint4*>(qb + (wo + 4u * c)) = make_uint4(word[c], word[c + 1], word[c + 2], word[c + 3]);
         } else {
 #pragma unroll
-            for (int c = 0; c < NC; ++c) dst[c] = word[c];
+            for (int c = 0; c < NC; ++c) *reinterpret_cast<uint32_t*>(qb + (wo + 4u * c)) = word[c];
         }
         if (part == 0) {
-            scales[g] = (uint16_t)f32_to_bf16(scale);
-            biases[g] = (uint16_t)f32_to_bf16(bias);
+            *reinterpret_cast<uint16_t*>(sb + g * 2u) = (uint16_t)f32_to_bf16(scale);
+            *reinterpret_cast<uint16_t*>(bb + g * 2u) = (uint16_t)f32_to_bf16(bias);
         }
     }
 }
 
-__global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w, int64_t n_groups,
+__global__ __launch_bounds__(256) void quantize_g64_kernel(const uint4* __restrict__ w, uint32_t n_groups,
                                                            uint32_t* __restrict__ wq,
                                                            uint16_t* __restrict__ scales,
                                                            uint16_t* __restrict__ biases) {
@@ -209,7 +218,7 @@ struct QuantBatch {
     uint32_t* wq[kQuantBatch];
     uint16_t* s[kQuantBatch];
     uint16_t* b[kQuantBatch];
-    int64_t n_groups[kQuantBatch];
+    uint32_t n_groups[kQuantBatch];
     int n;
 };
 
@@ -318,10 +327,16 @@ extern "C" int mq4_quantize(const uint16_t* w, int64_t N, int64_t K, int group_s
                     what);
     const int64_t n_groups = N * (K / 64);
     const int block = 256;
-    const int grid = grid_for(n_groups * kQuantLanesPerGroup, block, 256 * 32);
-    hipLaunchKernelGGL(quantize_g64_kernel, dim3(grid), dim3(block), 0, as_stream(stream),
-                       reinterpret_cast<const uint4*>(w), n_groups, wq, scales, biases);
-    return launch_status(what);
+    // pieces of at most kQuantMaxGroups groups (32-bit offsets in the kernel)
+    for (int64_t g0 = 0; g0 < n_groups; g0 += kQuantMaxGroups) {
+        const int64_t n = n_groups - g0 < kQuantMaxGroups ? n_groups - g0 : kQuantMaxGroups;
+        const int grid = grid_for(n * kQuantLanesPerGroup, block, 256 * 32);
+        hipLaunchKernelGGL(quantize_g64_kernel, dim3(grid), dim3(block), 0, as_stream(stream),
+                           reinterpret_cast<const uint4*>(w) + 8 * g0, (uint32_t)n, wq + 8 * g0, scales + g0,
+                           biases + g0);
+        if (int rc = launch_status(what)) return rc;
+    }
+    return ok();
 }
 
 extern "C" int mq4_quantize_batch(const mq4_quantize_job* jobs, int64_t n_jobs, int group_size, int bits,
@@ -345,24 +360,34 @@ extern "C" int mq4_quantize_batch(const mq4_quantize_job* jobs, int64_t n_jobs, 
                         "%s: job %lld: w must be 16-byte aligned, wq 4-byte, scales/biases 2-byte", what,
                         (long long)j);
     }
-    for (int64_t j0 = 0; j0 < n_jobs; j0 += kQuantBatch) {
-        QuantBatch a{};
-        a.n = (int)((n_jobs - j0) < kQuantBatch ? (n_jobs - j0) : kQuantBatch);
-        for (int i = 0; i < a.n; ++i) {
-            const mq4_quantize_job& q = jobs[j0 + i];
-            a.w[i] = reinterpret_cast<const uint4*>(q.w);
-            a.wq[i] = q.wq;
-            a.s[i] = q.scales;
-            a.b[i] = q.biases;
-            a.n_groups[i] = q.N * (q.K / 64);
-        }
-        // enough lanes to keep HBM busy, not more than the largest job uses
+    // the jobs' streams in pieces of at most kQuantMaxGroups groups (32-bit
+    // offsets in the kernel), kQuantBatch pieces per launch
+    QuantBatch a{};
+    auto flush = [&]() -> int {
+        if (a.n == 0) return 0;
+        // enough lanes to keep HBM busy, not more than the largest piece uses
         int64_t largest = 0;
         for (int i = 0; i < a.n; ++i) largest = a.n_groups[i] > largest ? a.n_groups[i] : largest;
         const int grid = grid_for(largest * kQuantLanesPerGroup, 256, 256 * 32);
         hipLaunchKernelGGL(quantize_g64_batch_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a);
-        if (int rc = launch_status(what)) return rc;
+        a = QuantBatch{};
+        return launch_status(what);
+    };
+    for (int64_t j = 0; j < n_jobs; ++j) {
+        const mq4_quantize_job& q = jobs[j];
+        const int64_t n_groups = q.N * (q.K / 64);
+        for (int64_t g0 = 0; g0 < n_groups; g0 += kQuantMaxGroups) {
+            const int i = a.n++;
+            a.w[i] = reinterpret_cast<const uint4*>(q.w) + 8 * g0;
+            a.wq[i] = q.wq + 8 * g0;
+            a.s[i] = q.scales + g0;
+            a.b[i] = q.biases + g0;
+            a.n_groups[i] = (uint32_t)(n_groups - g0 < kQuantMaxGroups ? n_groups - g0 : kQuantMaxGroups);
+            if (a.n == kQuantBatch)
+                if (int rc = flush()) return rc;
+        }
     }
+    if (int rc = flush()) return rc;
     return ok();
 }
 

@@ -186,6 +186,34 @@ def test_quantize_batch_matches_oracle(mq4, O, dev):
         assert torch.equal(sq, wq) and torch.equal(ss, s) and torch.equal(sb, b), i
 
 
+def test_quantize_stream_past_2_25_groups(mq4, O, dev):
+    """A matrix of 2^25 + 64 groups (4.3 GB of bf16): the kernels address one
+    stream by 32-bit byte offsets and the host splits longer streams at 2^25
+    groups.  The last rows, on both sides of the split, quantized within the
+    whole matrix (single call, and batched beside a small job) are
+    bit-identical to the same rows quantized alone and to the oracle."""
+    K = 2048
+    N = (1 << 25) // (K // 64) + 2                  # the split falls before row N - 2
+    print(f"quantize {N}x{K} (2^25 + 64 groups)", flush=True)
+    w = mq4.fill_normal_bf16((N, K), 3200, 0.0, 0.02, device=dev)
+    rows = slice(N - 4, N)
+    part = w[rows].contiguous()
+    pq, ps, pb = mq4.quantize(part)
+    wq, s, b = mq4.quantize(w)
+    torch.cuda.synchronize()
+    assert torch.equal(wq[rows], pq) and torch.equal(s[rows], ps) and torch.equal(b[rows], pb)
+    del wq, s, b
+    (bq0, bs0, bb0), (bq, bs, bb) = mq4.quantize_batch([part, w])
+    torch.cuda.synchronize()
+    assert torch.equal(bq[rows], pq) and torch.equal(bs[rows], ps) and torch.equal(bb[rows], pb)
+    assert torch.equal(bq0, pq) and torch.equal(bs0, ps) and torch.equal(bb0, pb)
+    rq, rs, rb = O.quantize(to_host_u16(part))
+    assert np.array_equal(words(pq), rq)
+    assert np.array_equal(to_host_u16(ps), rs) and np.array_equal(to_host_u16(pb), rb)
+    del w, bq, bs, bb
+    torch.cuda.empty_cache()
+
+
 def test_quantize_non_finite_groups(mq4, O, dev):
     """Groups holding +-inf, NaN (some or all elements) or extremes whose range
     overflows float32 (+-3e38): the kernel's guarded quotient path (any group
