@@ -366,7 +366,7 @@ def main():
         for name, fn in (("config1_gemv_gate", lambda: bench_gemv_gate(E, layers, x0)),
                          ("config2_mlp_chain", lambda: bench_mlp_chain(E, dec_layers, lm, norm_w, x0)),
                          ("config3_lm_head_argmax", lambda: bench_lm_head(E, lm, norm_w, x0)),
-                         ("config4_prefill", lambda: bench_prefill(E, layers, args)),
+                         ("config4_prefill", lambda: bench_prefill(E, layers, args, layer_norms)),
                          ("config5a_batched", lambda: bench_batched(E, layers, lm, norm_w, layer_norms)),
                          ("config5b_pack", lambda: bench_pack(E, layers, lm)),
                          ("next_q4_projections", lambda: bench_projections(E, x0)),
@@ -486,9 +486,11 @@ def bench_lm_head(E, lm, norm_w, x0):
                     "286 MB weight stream exceeds the last-level cache"}
 
 
-def bench_prefill(E, layers, args):
+def bench_prefill(E, layers, args, layer_norms):
     """Config 4: prefill Q4 GEMM (MFMA), M tokens through gate/up + SwiGLU
-    (6144x2048 x2) and down + residual (2048x6144), M in {1960, 2048, 8192}."""
+    (6144x2048 x2) and down + residual (2048x6144), M in {1960, 2048, 8192}:
+    the two entries separately, and the block's whole MLP half (RMSNorm +
+    gate/up + SwiGLU + down + residual) as one mq4_mlp_residual call."""
     torch, L, P, mq4 = E.torch, E.L, E.P, E.mq4
     g, u, d = layers[0]
     st = E.st()
@@ -497,18 +499,29 @@ def bench_prefill(E, layers, args):
         x = mq4.fill_normal_bf16((M, HID), mq4.STREAM_PREFILL, 0.0, 1.0, device=E.dev)
         h = torch.empty((M, INTER), dtype=torch.bfloat16, device=E.dev)
         y = torch.empty((M, HID), dtype=torch.bfloat16, device=E.dev)
+        wsb = L.mq4_mlp_workspace_size(M, HID, INTER)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=E.dev)
         reps = 3 if M == 8192 else 10
         us_gu = E.timed(lambda: L.mq4_mlp_gate_up_silu(P(x.data_ptr()), M, HID, *g.ptrs(), *u.ptrs(), INTER,
                                                        P(h.data_ptr()), st), reps, warm=2)
         us_dn = E.timed(lambda: L.mq4_qmm_residual(P(h.data_ptr()), M, INTER, *d.ptrs(), HID, P(x.data_ptr()),
                                                    P(y.data_ptr()), st), reps, warm=2)
+        us_one = E.timed(lambda: L.mq4_mlp_residual(P(x.data_ptr()), M, HID, P(layer_norms[0].data_ptr()), 1e-6,
+                                                    *g.ptrs(), *u.ptrs(), *d.ptrs(), INTER, P(ws.data_ptr()), wsb,
+                                                    P(y.data_ptr()), st), reps, warm=2)
         f_gu, f_dn = 2 * 2.0 * M * INTER * HID, 2.0 * M * HID * INTER
         out[str(M)] = {"gate_up_silu_us": round(us_gu, 1), "gate_up_silu": mfma_roofline(f_gu, us_gu),
                        "down_residual_us": round(us_dn, 1), "down_residual": mfma_roofline(f_dn, us_dn),
-                       "mlp_us": round(us_gu + us_dn, 1), "mlp": mfma_roofline(f_gu + f_dn, us_gu + us_dn)}
-        del x, h, y
+                       "mlp_us": round(us_gu + us_dn, 1), "mlp": mfma_roofline(f_gu + f_dn, us_gu + us_dn),
+                       "mlp_residual_one_call_us": round(us_one, 1),
+                       "mlp_residual_one_call": mfma_roofline(f_gu + f_dn, us_one)}
+        del x, h, y, ws
     return {"shapes": "M x 2048 @ gate/up 6144x2048 (fused SwiGLU), M x 6144 @ down 2048x6144 (+ residual)",
-            "flops": "2*M*N*K per matrix (algorithmic, bf16 MFMA peak 2.5 PFLOP/s dense)", "M": out}
+            "flops": "2*M*N*K per matrix (algorithmic, bf16 MFMA peak 2.5 PFLOP/s dense)",
+            "mlp_residual_one_call": "mq4_mlp_residual: RMSNorm(1+w) + gate/up + SwiGLU + down + residual in one "
+                                     "call (pre-pass of the normalized x in the MFMA operand order, h written so by "
+                                     "the SwiGLU epilogue; the norm's work counted in the time, not the flops)",
+            "M": out}
 
 
 def bench_batched(E, layers, lm, norm_w, layer_norms):
@@ -695,9 +708,14 @@ def profile_mode(args, E, layers, lm, norm_w, layer_norms, x0, dstep, dargs):
         x = mq4.fill_normal_bf16((M, HID), mq4.STREAM_PREFILL, 0.0, 1.0, device=E.dev)
         h = torch.empty((M, INTER), dtype=torch.bfloat16, device=E.dev)
         y = torch.empty((M, HID), dtype=torch.bfloat16, device=E.dev)
+        wsb = L.mq4_mlp_workspace_size(M, HID, INTER)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=E.dev)
         for _ in range(n):
             L.mq4_mlp_gate_up_silu(P(x.data_ptr()), M, HID, *g.ptrs(), *u.ptrs(), INTER, P(h.data_ptr()), st)
             L.mq4_qmm_residual(P(h.data_ptr()), M, INTER, *d.ptrs(), HID, P(x.data_ptr()), P(y.data_ptr()), st)
+            # the same MLP half as one call (norm pre-pass, paired operands)
+            L.mq4_mlp_residual(P(x.data_ptr()), M, HID, P(layer_norms[0].data_ptr()), 1e-6, *g.ptrs(), *u.ptrs(),
+                               *d.ptrs(), INTER, P(ws.data_ptr()), wsb, P(y.data_ptr()), st)
     elif k == "batched":
         M = args.batched_m
         x = mq4.fill_normal_bf16((M, HID), 3000, 0.0, 1.0, device=E.dev)

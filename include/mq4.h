@@ -34,6 +34,8 @@
  *   mq4_rmsnorm_gate_up_silu  the same after rms_norm (src/model/marlin.cpp:141)
  *   mq4_swiglu_bf16      swiglu(gate, up) (src/model/marlin.cpp:27-29)
  *   mq4_qmm_residual     hidden + qmatmul(h, down)
+ *   mq4_mlp_residual     hidden + mlp_forward(rms_norm(hidden)) in one call
+ *                        (src/model/marlin.cpp:141-142, 31-35)
  *                        (src/model/marlin.cpp:34, 142)
  *   mq4_lm_head_argmax   sample_token(lm_head(h)) with temperature <= 0
  *                        (src/model/marlin.cpp:161-169,
@@ -163,6 +165,32 @@ int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
                              const uint32_t* up_wq, const uint16_t* up_scales,
                              const uint16_t* up_biases,
                              int64_t N, uint16_t* h, void* stream);
+
+/* One transformer block's MLP half: y = x + down(swiglu(gate(n), up(n))),
+ * n = rms_norm(x) with the (1 + w) multiplier, i.e. rms_norm (marlin.cpp:141,
+ * 12-16), mlp_forward (:31-35) and the residual add (:142) of
+ * text_forward_embeddings, for M rows.  gate and up are [N, K], down [K, N];
+ * norm_weight is bf16 [K], 16-byte aligned.  The result is within the GEMM
+ * bar of the chain mq4_rmsnorm_gate_up_silu + mq4_qmm_residual (the same
+ * normalized operand and bf16 h; fp32 sums in another order, so not always
+ * bit for bit).  From M = 33 rows on (K and N multiples of 512, scale and
+ * bias rows 4-byte aligned) it runs the MFMA GEMM on activations stored in
+ * the matrix cores' operand order with their group sums: a pre-pass writes
+ * the normalized x so, the SwiGLU epilogue writes h so.  workspace: at least
+ * mq4_mlp_workspace_size(M, K, N) bytes, 256-byte aligned, no
+ * initialisation; calls that overlap in time need separate workspaces.  y
+ * may equal x (in place). */
+size_t mq4_mlp_workspace_size(int64_t M, int64_t K, int64_t N);
+int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K,
+                     const uint16_t* norm_weight, float eps,
+                     const uint32_t* gate_wq, const uint16_t* gate_scales,
+                     const uint16_t* gate_biases,
+                     const uint32_t* up_wq, const uint16_t* up_scales,
+                     const uint16_t* up_biases,
+                     const uint32_t* down_wq, const uint16_t* down_scales,
+                     const uint16_t* down_biases,
+                     int64_t N, void* workspace, size_t workspace_bytes,
+                     uint16_t* y, void* stream);
 
 /* out[i] = bf16(bf16(bf16(sigmoid(gate[i])) * gate[i]) * up[i]): the
  * unfused swiglu (src/model/marlin.cpp:27-29) over n bf16 elements. */

@@ -31,6 +31,7 @@ __all__ = [
     "MQ4Error", "library_path", "lib", "QuantizedTensor", "MLPWeights",
     "quantize", "dequantize", "quantized_matmul", "quantized_matmul_f32", "argmax", "swiglu",
     "quantize_weight", "quantize_batch", "quantize_weights", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
+    "mlp_residual",
     "lm_head", "lm_head_argmax", "lm_head_last_row", "sample_token", "rms_norm", "fill_normal_bf16",
     "DecoderLayer", "DecodeStep", "save_q4_cache", "load_q4_cache", "quantize_or_load",
 ]
@@ -102,6 +103,8 @@ def lib():
         "mq4_qmm_f32": ([P, I64, I64, P, P, P, I64, P, P], I),
         "mq4_mlp_gate_up_silu": ([P, I64, I64, P, P, P, P, P, P, I64, P, P], I),
         "mq4_rmsnorm_gate_up_silu": ([P, I64, I64, P, ctypes.c_float, P, P, P, P, P, P, I64, P, P], I),
+        "mq4_mlp_workspace_size": ([I64, I64, I64], ctypes.c_size_t),
+        "mq4_mlp_residual": ([P, I64, I64, P, ctypes.c_float] + [P] * 9 + [I64, P, ctypes.c_size_t, P, P], I),
         "mq4_rmsnorm_lm_head_argmax": ([P, I64, I64, P, ctypes.c_float, P, P, P, I64, P, P, P, SZ, P], I),
         "mq4_swiglu_bf16": ([P, P, I64, P, P], I),
         "mq4_lm_head_argmax_workspace_size": ([I64, I64], SZ),
@@ -440,11 +443,47 @@ def mlp_forward(x: torch.Tensor, w: MLPWeights, residual: torch.Tensor | None = 
                 norm_weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
     """src/model/marlin.cpp:31-35 (down(swiglu(gate x, up x))); with `residual`
     also the add of src/model/marlin.cpp:142, with `norm_weight` the rms_norm
-    of src/model/marlin.cpp:141 in front."""
+    of src/model/marlin.cpp:141 in front.  With both and residual is x (the
+    block's hidden state, :141-142), one mq4_mlp_residual call."""
+    if residual is not None and norm_weight is not None and residual is x:
+        return mlp_residual(x, w, norm_weight, eps)
     h = mlp_gate_up_silu(x, w.gate_proj, w.up_proj, norm_weight, eps)
     if residual is None:
         return qmatmul(h, w.down_proj)
     return qmatmul_residual(h, w.down_proj, residual)
+
+
+def mlp_residual(x: torch.Tensor, w: MLPWeights, norm_weight: torch.Tensor, eps: float = 1e-6,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """x + mlp_forward(rms_norm(x, norm_weight)) (src/model/marlin.cpp:141-142,
+    31-35) in one mq4_mlp_residual call; out may be x (in place)."""
+    fn = "mlp_residual"
+    for q in (w.gate_proj, w.up_proj, w.down_proj):
+        _require_quantized(q, fn)
+    Kx = _in_features(fn, x)
+    N = _check_weight(fn, w.gate_proj.weight, w.gate_proj.scales, w.gate_proj.biases, Kx, w.gate_proj.group_size,
+                      w.gate_proj.bits)
+    if _check_weight(fn, w.up_proj.weight, w.up_proj.scales, w.up_proj.biases, Kx, w.up_proj.group_size,
+                     w.up_proj.bits) != N:
+        raise ValueError(f"{fn}: gate and up have different output sizes")
+    if _check_weight(fn, w.down_proj.weight, w.down_proj.scales, w.down_proj.biases, N, w.down_proj.group_size,
+                     w.down_proj.bits) != Kx:
+        raise ValueError(f"{fn}: down_proj must map {N} back to {Kx} features")
+    _check_vector(fn, norm_weight, Kx, "norm_weight")
+    norm_weight = _need(norm_weight, torch.bfloat16, "norm_weight")
+    x = _need(x, torch.bfloat16, "x")
+    K = x.shape[-1]
+    M = x.numel() // K
+    y = torch.empty_like(x) if out is None else _need(out, torch.bfloat16, "out")
+    if y.shape != x.shape:
+        raise ValueError(f"{fn}: out has shape {tuple(y.shape)}, x {tuple(x.shape)}")
+    L = lib()
+    ws_bytes = L.mq4_mlp_workspace_size(M, K, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    qa = lambda q: (_ptr(q.weight), _ptr(q.scales), _ptr(q.biases))
+    _check(L.mq4_mlp_residual(_ptr(x), M, K, _ptr(norm_weight), eps, *qa(w.gate_proj), *qa(w.up_proj),
+                              *qa(w.down_proj), N, _ptr(ws), ws_bytes, _ptr(y), _stream(x.device)))
+    return y
 
 
 def lm_head(hidden: torch.Tensor, w: QuantizedTensor) -> torch.Tensor:

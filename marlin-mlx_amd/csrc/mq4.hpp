@@ -191,6 +191,29 @@ inline Result<int> mlp_forward_residual(uint16_t* hidden, int64_t M, const uint1
     return 0;
 }
 
+// hidden = hidden + mlp_forward(rms_norm(hidden, norm_weight)) in one call
+// (src/model/marlin.cpp:141-142, 31-35), in place; the workspace holds
+// mq4_mlp_workspace_size(max_rows, hidden size, intermediate size) bytes.
+class MlpResidual {
+public:
+    MlpResidual(int64_t max_rows, int64_t hidden, int64_t intermediate)
+        : ws_(mq4_mlp_workspace_size(max_rows, hidden, intermediate)), max_rows_(max_rows) {}
+    Result<int> operator()(uint16_t* x, int64_t M, const uint16_t* norm_weight, float eps, const MLPWeights& w,
+                           hipStream_t stream) {
+        if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "MlpResidual: M exceeds max_rows"};
+        const int rc = mq4_mlp_residual(x, M, w.gate_proj.in_features, norm_weight, eps, w.gate_proj.wq(),
+                                        w.gate_proj.s(), w.gate_proj.b(), w.up_proj.wq(), w.up_proj.s(),
+                                        w.up_proj.b(), w.down_proj.wq(), w.down_proj.s(), w.down_proj.b(),
+                                        w.gate_proj.out_features, ws_.get(), ws_.bytes(), x, stream);
+        if (rc != MQ4_OK) return last_error(rc);
+        return 0;
+    }
+
+private:
+    DeviceBuffer ws_;
+    int64_t max_rows_;
+};
+
 // Greedy next token(s): idx[m] = argmax(lm_head(rms_norm(hidden))) for each
 // of the M rows (src/model/marlin.cpp:145, 161-169; src/sampling/sampler.cpp:14-16).
 class GreedyLmHead {

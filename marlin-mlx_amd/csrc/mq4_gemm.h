@@ -23,10 +23,26 @@ struct GemmArgs {
     const uint16_t* res;     // GEMM_RESIDUAL: [M, N]
     const uint16_t* norm_w;  // fused (1 + w) RMSNorm of x: [K] bf16, 16-byte aligned
     float eps;
+    // Non-null: x is already in the MFMA operand order (every 8-element chunk
+    // as (x0, x4, x1, x5, x2, x6, x3, x7), as launch_pair_rows writes it) and
+    // xsum[g * M + m] is the fp32 sum of group g of row m (group-major).
+    const float* xsum;
+    // GEMM_SWIGLU, non-null (with K/64 even, N % 64 == 0): y is written in
+    // that same operand order and ysum[g * M + m] = the fp32 sum of group g
+    // of row m of y, ready to be the x / xsum of the next product.
+    float* ysum;
 };
 
 // Enqueue Y = epilogue(X . W^T) on `st` (X = rms_norm(x) with norm, for the
-// GEMM_STORE and GEMM_SWIGLU epilogues); 0, or -1 for an unsupported pair.
+// GEMM_STORE and GEMM_SWIGLU epilogues); 0, or -1 for an unsupported pair
+// (a.xsum set: no fused norm, K/64 even, scale/bias rows 4-byte aligned).
 int launch_q4_gemm(const GemmArgs& a, int epi, bool norm, hipStream_t st);
+
+// xp = x (norm_w null) or bf16(x * rsqrt(mean(x^2) + eps) * (1 + norm_w)),
+// the bits of mq4_rms_norm, with every 8-element chunk of a row in the
+// pair order above, and xs[g * M + m] = the fp32 sum of group g of row m
+// of xp (group-major).  K % 512 == 0; x, xp, norm_w 16-byte aligned.
+int launch_pair_rows(const uint16_t* x, int M, int K, const uint16_t* norm_w, float eps, uint16_t* xp, float* xs,
+                     hipStream_t st);
 
 }  // namespace mq4

@@ -329,12 +329,13 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
     __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
 }
 
-template <int WM, int WN>
+template <int WM, int WN, bool PRE>
 struct Stage {
     static constexpr int BM = 64 * WM, BNW = 64 * WN;
     uint4 a[BM * 8];                      // [row][chunk ^ ((row >> 1) & 7)]
     uint4 b[2 * BNW];                     // [k-half][weight row]
     uint32_t sb[2][BNW];                  // scales, biases: groups (g & ~1, g | 1)
+    float xs[PRE ? BM : 1];               // PRE: the rows' group sums X
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -342,7 +343,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // v_perm_b32 selectors: (lo half of x, lo half of z) and (hi of x, hi of z)
 constexpr uint32_t kPermLo = 0x05040100u, kPermHi = 0x07060302u;
 
-template <int EPI, int WM, int WN, int S>
+template <int EPI, int WM, int WN, int S, bool PRE>
 __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p) {
 #pragma clang fp contract(off)
     constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
@@ -351,9 +352,14 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
     constexpr int A_I = TBM * 8 / (64 * NW);            // activation DMA instructions per wave and group
     constexpr int B_I = 2 * BNW / (64 * NW);            // weight
     constexpr int SB_I = 2 * BNW / (64 * NW);           // scale/bias
-    constexpr int kDmaPerWave = A_I + B_I + SB_I;
+    // PRE: the rows' group sums travel with the tile, 64 rows per DMA
+    // instruction, issued by the first TBM / 64 waves (with S = 2 every step
+    // waits for all of a wave's DMA, so the counts need not match)
+    constexpr int X_I = PRE ? 1 : 0;
+    static_assert(!PRE || (S == 2 && TBM / 64 <= NW), "group-sum DMA");
+    constexpr int kDmaPerWave = A_I + B_I + SB_I + X_I;
     static_assert(A_I * 64 * NW == TBM * 8 && B_I * 64 * NW == 2 * BNW, "DMA split");
-    typedef Stage<WM, WN> St;
+    typedef Stage<WM, WN, PRE> St;
     static_assert(S == 2 || S == 3, "ring stages");
     static_assert((size_t)S * sizeof(St) <= 65536, "LDS DMA targets must lie in the first 64 KiB");
     typedef typename std::conditional<S == 3, St, char>::type St2;   // no third stage with S = 2
@@ -419,7 +425,18 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
         sbbase[t] = reinterpret_cast<const char*>(sel ? mat_of(r0).b : mat_of(r0).s);
         sboff[t] = (uint32_t)((int64_t)wrow_of(r0 + lane) * G * 2);
     }
+    // PRE: group sum of row m0 + 64 wave + lane, group g (clamped row); the
+    // sums are group-major, so one instruction reads 256 contiguous bytes
+    const char* const xsbase = reinterpret_cast<const char*>(p.xsum);
+    uint32_t xsoff = 0;
+    if constexpr (PRE) {
+        const int r = m0 + 64 * wave + lane;
+        xsoff = (uint32_t)((r < M ? r : M - 1) * 4);
+    }
     auto issue = [&](int g, St& st) {
+        if constexpr (PRE) {
+            if (wave < TBM / 64) lds_dma4(xsbase + (int64_t)g * M * 4 + xsoff, &st.xs[64 * wave]);
+        }
 #pragma unroll
         for (int t = 0; t < A_I; ++t)
             lds_dma16(xbase + g * 128 + aoff[t], &st.a[(wave * A_I + t) * 64]);
@@ -469,13 +486,17 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
             for (int i = 0; i < 2; ++i) {
                 const int r = wm * 64 + i * 32 + col, ch = 4 * h + ks;
                 const uint4 raw = st.a[r * 8 + (ch ^ ((r >> 1) & 7))];
-                xs[i] = dot2_bf16(raw.w, ONES, dot2_bf16(raw.z, ONES, dot2_bf16(raw.y, ONES, dot2_bf16(raw.x, ONES, xs[i]))));
-                // nibble-pair order (x0, x4), (x1, x5), (x2, x6), (x3, x7)
-                const uint4 pr = make_uint4(__builtin_amdgcn_perm(raw.z, raw.x, kPermLo),
-                                            __builtin_amdgcn_perm(raw.z, raw.x, kPermHi),
-                                            __builtin_amdgcn_perm(raw.w, raw.y, kPermLo),
-                                            __builtin_amdgcn_perm(raw.w, raw.y, kPermHi));
-                a[i] = __builtin_bit_cast(bf16x8_t, pr);
+                if constexpr (PRE) {
+                    a[i] = __builtin_bit_cast(bf16x8_t, raw);          // already in pair order
+                } else {
+                    xs[i] = dot2_bf16(raw.w, ONES, dot2_bf16(raw.z, ONES, dot2_bf16(raw.y, ONES, dot2_bf16(raw.x, ONES, xs[i]))));
+                    // nibble-pair order (x0, x4), (x1, x5), (x2, x6), (x3, x7)
+                    const uint4 pr = make_uint4(__builtin_amdgcn_perm(raw.z, raw.x, kPermLo),
+                                                __builtin_amdgcn_perm(raw.z, raw.x, kPermHi),
+                                                __builtin_amdgcn_perm(raw.w, raw.y, kPermLo),
+                                                __builtin_amdgcn_perm(raw.w, raw.y, kPermHi));
+                    a[i] = __builtin_bit_cast(bf16x8_t, pr);
+                }
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) b[j] = weight_operand_k(word_of(bw[j], ks), nib_mask, nib_exp);
@@ -488,7 +509,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
         mfma_result_pad();
         float X[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) X[i] = xs[i] + __shfl_xor(xs[i], 32);
+        for (int i = 0; i < 2; ++i) {
+            if constexpr (PRE) X[i] = st.xs[wm * 64 + i * 32 + col];
+            else X[i] = xs[i] + __shfl_xor(xs[i], 32);
+        }
         // acc += s * D (VALU) ...
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -550,14 +574,29 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
     wait_vmcnt<0>();                                 // no DMA outstanding past the loop
 
     // ---- epilogue: lane l of a 32 x 32 tile holds rows (e/4)*8 + (l/32)*4 + e%4, column l%32 ----
+    // SwiGLU with ysum: the block's BN = 64 output columns are one group of y;
+    // y goes out in the operand order (column c of a chunk at 2 (c % 4) + c / 4)
+    // and the group sums of its rows through LDS (ring stage 0, free now)
+    const bool paired_out = EPI == GEMM_SWIGLU && p.ysum != nullptr;
+    uint16_t* tile = reinterpret_cast<uint16_t*>(&st0);          // [TBM][72] bf16
+    static_assert(TBM * 72 * 2 <= (int)sizeof(St), "epilogue tile");
+    if (paired_out) __syncthreads();                               // every wave is done with the ring
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
             const int cn = NMAT == 2 ? n0 + wn * 32 + col : n0 + wn * 64 + j * 32 + col;
+            const int cw = paired_out ? ((cn & ~7) | (2 * (cn & 3) + ((cn >> 2) & 1))) : cn;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
+                const int rl = wm * 64 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
+                const int row = m0 + rl;
+                if (EPI == GEMM_SWIGLU) {
+                    const uint32_t v = swiglu_bf16(acc[i][0][e], acc[i][1][e]);
+                    if (paired_out) tile[rl * 72 + wn * 32 + col] = (uint16_t)v;
+                    if (row < M && cn < N) reinterpret_cast<uint16_t*>(p.y)[(int64_t)row * N + cw] = (uint16_t)v;
+                    continue;
+                }
                 if (row >= M || cn >= N) continue;
                 const int64_t o = (int64_t)row * N + cn;
                 const float v = acc[i][j][e];
@@ -565,14 +604,32 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
                     reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)f32_to_bf16(v);
                 } else if (EPI == GEMM_STORE_F32) {
                     reinterpret_cast<float*>(p.y)[o] = v;
-                } else if (EPI == GEMM_RESIDUAL) {
+                } else {
                     reinterpret_cast<uint16_t*>(p.y)[o] =
                         (uint16_t)f32_to_bf16(bf16_to_f32(p.res[o]) + round_bf16(v));
-                } else {
-                    reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)swiglu_bf16(v, acc[i][1][e]);
                 }
             }
         }
+    if (paired_out) {
+        __syncthreads();
+        // thread t: half t % 2 of row t / 2 of the tile (32 values), summed
+        // left to right, then the two halves
+        static_assert(64 * NW == 2 * TBM, "two threads per row");
+        const int rl = threadIdx.x >> 1, half = threadIdx.x & 1;
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 v = *reinterpret_cast<const uint4*>(&tile[rl * 72 + half * 32 + c * 8]);
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sum += bf16_to_f32(w4[q] & 0xffffu);
+                sum += bf16_to_f32(w4[q] >> 16);
+            }
+        }
+        sum += __shfl_xor(sum, 1);
+        if (half == 0 && m0 + rl < M) p.ysum[(int64_t)(n0 >> 6) * M + m0 + rl] = sum;
+    }
 }
 
 // Blocks of the (WM, WN) layout for an M x N product.
@@ -582,9 +639,9 @@ unsigned blocks_of(int M, int N) {
     return (unsigned)(((N + BN - 1) / BN) * ((M + 64 * WM - 1) / (64 * WM)));
 }
 
-template <int EPI, int WM, int WN, int S>
+template <int EPI, int WM, int WN, int S, bool PRE>
 void launch_dma(const GemmArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((q4_gemm_dma_kernel<EPI, WM, WN, S>), dim3(blocks_of<EPI, WM, WN>(a.M, a.N)),
+    hipLaunchKernelGGL((q4_gemm_dma_kernel<EPI, WM, WN, S, PRE>), dim3(blocks_of<EPI, WM, WN>(a.M, a.N)),
                        dim3(64 * WM * WN), 0, st, a);
 }
 
@@ -594,13 +651,14 @@ void launch_dma(const GemmArgs& a, hipStream_t st) {
 // down (N = 2048) products, with the least LDS (41 KB, so two blocks per CU).
 template <int EPI>
 void launch_dma_auto(const GemmArgs& a, hipStream_t st) {
-    launch_dma<EPI, 2, 2, 2>(a, st);
+    if (a.xsum) launch_dma<EPI, 2, 2, 2, true>(a, st);
+    else launch_dma<EPI, 2, 2, 2, false>(a, st);
 }
 
 }  // namespace dma
 
 template <int EPI, bool NORM>
-void launch(const GemmArgs& a, hipStream_t st) {
+int launch(const GemmArgs& a, hipStream_t st) {
     constexpr int BN = EPI == GEMM_SWIGLU ? 64 : 128;
     const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM));
     // the DMA kernel addresses x and the weights by 32-bit byte offsets
@@ -609,10 +667,19 @@ void launch(const GemmArgs& a, hipStream_t st) {
                         reinterpret_cast<uintptr_t>(a.A.b) % 4 == 0 &&
                         (EPI != GEMM_SWIGLU ||
                          (reinterpret_cast<uintptr_t>(a.B.s) % 4 == 0 && reinterpret_cast<uintptr_t>(a.B.b) % 4 == 0));
+    // paired output (ysum): the DMA kernel's SwiGLU epilogue only
+    if (a.ysum && (EPI != GEMM_SWIGLU || NORM || !dma_ok || a.N % 64 != 0)) return -1;
+    if (a.xsum || a.ysum) {
+        // pre-paired activations: the DMA kernel only
+        if (NORM || !dma_ok) return -1;
+        dma::launch_dma_auto<EPI>(a, st);
+        return 0;
+    }
     if (NORM || !dma_ok)
         hipLaunchKernelGGL((q4_gemm_kernel<EPI, NORM>), dim3(blocks), dim3(kThreads), 0, st, a);
     else
         dma::launch_dma_auto<EPI>(a, st);
+    return 0;
 }
 
 }  // namespace gemm
@@ -620,19 +687,75 @@ void launch(const GemmArgs& a, hipStream_t st) {
 int launch_q4_gemm(const GemmArgs& a, int epi, bool norm, hipStream_t st) {
     if (norm) {
         switch (epi) {
-            case GEMM_STORE: gemm::launch<GEMM_STORE, true>(a, st); break;
-            case GEMM_SWIGLU: gemm::launch<GEMM_SWIGLU, true>(a, st); break;
+            case GEMM_STORE: return gemm::launch<GEMM_STORE, true>(a, st);
+            case GEMM_SWIGLU: return gemm::launch<GEMM_SWIGLU, true>(a, st);
             default: return -1;
         }
-        return 0;
     }
     switch (epi) {
-        case GEMM_STORE: gemm::launch<GEMM_STORE, false>(a, st); break;
-        case GEMM_STORE_F32: gemm::launch<GEMM_STORE_F32, false>(a, st); break;
-        case GEMM_RESIDUAL: gemm::launch<GEMM_RESIDUAL, false>(a, st); break;
-        case GEMM_SWIGLU: gemm::launch<GEMM_SWIGLU, false>(a, st); break;
+        case GEMM_STORE: return gemm::launch<GEMM_STORE, false>(a, st);
+        case GEMM_STORE_F32: return gemm::launch<GEMM_STORE_F32, false>(a, st);
+        case GEMM_RESIDUAL: return gemm::launch<GEMM_RESIDUAL, false>(a, st);
+        case GEMM_SWIGLU: return gemm::launch<GEMM_SWIGLU, false>(a, st);
         default: return -1;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Activation pre-pass (launch_pair_rows): one wave per row, lane l takes the
+// 8-element chunks l, l + 64, ...; with the norm a first pass forms the
+// row's sum of squares (each lane its chunks, then the wave), with the
+// per-element formula of mq4_rms_norm.  The 8 chunks of a group are 8
+// consecutive lanes: their chunk sums are added over the lane pairs, quads
+// and octets.  The sums are stored group-major: xs[g * M + m].
+template <bool NORM>
+__global__ __launch_bounds__(256) void pair_rows_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                        const uint16_t* __restrict__ nw, float eps,
+                                                        uint16_t* __restrict__ xp, float* __restrict__ xs) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;                                  // whole waves
+    const int CH = K / 8, G = K / 64;
+    const uint4* src = reinterpret_cast<const uint4*>(x + (int64_t)m * K);
+    uint4* dst = reinterpret_cast<uint4*>(xp + (int64_t)m * K);
+    float r = 0.0f;
+    if (NORM) {
+        float ss = 0.0f;
+        for (int c = lane; c < CH; c += 64) {
+            const uint4 v = src[c];
+            ss = sumsq_word(ss, v.x);
+            ss = sumsq_word(ss, v.y);
+            ss = sumsq_word(ss, v.z);
+            ss = sumsq_word(ss, v.w);
+        }
+        r = rms_inv(wave_sum(ss), K, eps);
+    }
+    for (int c = lane; c < CH; c += 64) {
+        uint4 v = src[c];
+        if (NORM) {
+            const uint4 w = reinterpret_cast<const uint4*>(nw)[c];
+            v = make_uint4(norm_word(v.x, w.x, r), norm_word(v.y, w.y, r), norm_word(v.z, w.z, r),
+                           norm_word(v.w, w.w, r));
+        }
+        uint32_t pr[4];
+        float sum = pair_chunk(v, pr, 0.0f);
+        dst[c] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 4);
+        if ((lane & 7) == 0) xs[(int64_t)(c >> 3) * M + m] = sum;
+    }
+}
+
+int launch_pair_rows(const uint16_t* x, int M, int K, const uint16_t* norm_w, float eps, uint16_t* xp, float* xs,
+                     hipStream_t st) {
+    if (M < 1 || K % 512 != 0) return -1;
+    const unsigned blocks = (unsigned)((M + 3) / 4);
+    if (norm_w)
+        hipLaunchKernelGGL(pair_rows_kernel<true>, dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps, xp, xs);
+    else
+        hipLaunchKernelGGL(pair_rows_kernel<false>, dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps, xp, xs);
     return 0;
 }
 

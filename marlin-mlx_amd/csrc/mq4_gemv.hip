@@ -742,6 +742,102 @@ extern "C" int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
                               gate_biases, up_wq, up_scales, up_biases, N, h, stream);
 }
 
+namespace mq4 {
+
+// ---- rms_norm + mlp_forward + residual in one call ----
+// Workspace: h [M, N] bf16; on the GEMM path h is written in the GEMM's
+// operand order by the SwiGLU epilogue, and the normalized x (by
+// launch_pair_rows) too, both with their fp32 group sums, so neither GEMM
+// forms them per wave.  Sections 256-byte aligned.
+struct MlpWs {
+    uint16_t* h = nullptr;
+    uint16_t* xp = nullptr;
+    float* xs = nullptr;
+    uint16_t* hp = nullptr;
+    float* hs = nullptr;
+    size_t bytes = 0;
+};
+
+static MlpWs mlp_ws_layout(void* base, int64_t M, int64_t K, int64_t N) {
+    MlpWs w;
+    char* b = reinterpret_cast<char*>(base);
+    size_t off = 0;
+    auto take = [&](size_t n) -> char* {
+        char* q = b ? b + off : nullptr;
+        off += (n + 255) & ~(size_t)255;
+        return q;
+    };
+    // h (the other path's natural h, or the paired h)
+    w.h = w.hp = reinterpret_cast<uint16_t*>(take((size_t)M * N * 2));
+    if (M >= kGemmMinM) {
+        w.xp = reinterpret_cast<uint16_t*>(take((size_t)M * K * 2));
+        w.xs = reinterpret_cast<float*>(take((size_t)M * (K / 64) * 4));
+        w.hs = reinterpret_cast<float*>(take((size_t)M * (N / 64) * 4));
+    }
+    w.bytes = off;
+    return w;
+}
+
+// The pre-paired GEMM path: K and N multiples of 512 (whole waves of chunks
+// in launch_pair_rows, an even group count), scale/bias rows 4-byte aligned,
+// byte offsets within 32 bits.
+static bool mlp_paired_ok(int64_t M, int64_t K, int64_t N, const QMat& g, const QMat& u, const QMat& d) {
+    auto a4 = [](const QMat& q) { return aligned(q.s, 4) && aligned(q.b, 4); };
+    return M >= kGemmMinM && K % 512 == 0 && N % 512 == 0 && a4(g) && a4(u) && a4(d) &&
+           M * N * 2 <= 0xFFFFFFFFLL && N * K / 2 <= 0xFFFFFFFFLL;
+}
+
+}  // namespace mq4
+
+extern "C" size_t mq4_mlp_workspace_size(int64_t M, int64_t K, int64_t N) {
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    return mlp_ws_layout(nullptr, M, K, N).bytes;
+}
+
+extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_weight, float eps,
+                                const uint32_t* gate_wq, const uint16_t* gate_scales, const uint16_t* gate_biases,
+                                const uint32_t* up_wq, const uint16_t* up_scales, const uint16_t* up_biases,
+                                const uint32_t* down_wq, const uint16_t* down_scales, const uint16_t* down_biases,
+                                int64_t N, void* workspace, size_t workspace_bytes, uint16_t* y, void* stream) {
+    const char* what = "mq4_mlp_residual";
+    if (int rc = check_qmm_args(what, x, M, K, gate_wq, gate_scales, gate_biases, N)) return rc;
+    if (int rc = check_qmm_args(what, x, M, K, up_wq, up_scales, up_biases, N)) return rc;
+    if (int rc = check_norm(what, norm_weight, eps)) return rc;
+    if (!y || !aligned(y, 2)) return fail(MQ4_ERR_INVALID_ARG, "%s: y must be a 2-byte aligned pointer", what);
+    const size_t need = mlp_ws_layout(nullptr, M, K, N).bytes;
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+        return fail(MQ4_ERR_WORKSPACE, "%s: workspace needs %zu bytes, 256-byte aligned (got %zu)", what, need,
+                    workspace_bytes);
+    const MlpWs w = mlp_ws_layout(workspace, M, K, N);
+    if (int rc = check_qmm_args(what, w.h, M, N, down_wq, down_scales, down_biases, K)) return rc;
+    const QMat G{gate_wq, gate_scales, gate_biases}, U{up_wq, up_scales, up_biases},
+        D{down_wq, down_scales, down_biases};
+    hipStream_t st = as_stream(stream);
+    if (mlp_paired_ok(M, K, N, G, U, D)) {
+        if (launch_pair_rows(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
+            return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+        // gate/up + SwiGLU writes h already paired, with its group sums
+        GemmArgs gu{w.xp, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, nullptr, 0.0f, w.xs, w.hs};
+        if (launch_q4_gemm(gu, GEMM_SWIGLU, false, st)) return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+        GemmArgs dn{w.hp, (int)M, (int)K, (int)N, D, QMat{nullptr, nullptr, nullptr}, y, x, nullptr, 0.0f, w.hs, nullptr};
+        if (launch_q4_gemm(dn, GEMM_RESIDUAL, false, st)) return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+        return launch_status(what);
+    }
+    // otherwise the separate entries' kernels: norm + gate/up + SwiGLU into h,
+    // then down + residual
+    if (int rc = gate_up_impl<true>(what, x, M, K, norm_weight, eps, gate_wq, gate_scales, gate_biases, up_wq,
+                                    up_scales, up_biases, N, w.h, stream))
+        return rc;
+    GemvParams a = params(w.h, M, N, K, D, {nullptr, nullptr, nullptr}, y);
+    a.res = x;
+    if (M >= kGemmMinM) {
+        run_gemm(a, M, GEMM_RESIDUAL, st);
+        return launch_status(what);
+    }
+    if (run_small<EPI_RESIDUAL, false>(a, (int)M, st)) return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported K", what);
+    return launch_status(what);
+}
+
 extern "C" size_t mq4_lm_head_argmax_workspace_size(int64_t M, int64_t N) {
     (void)N;
     return lm_head_ws_bytes(M);

@@ -66,12 +66,16 @@ int main(int argc, char** argv) {
         if (it == loaded.value().end()) return 5;
         lmq.value() = std::move(it->second);
     }
-    mq4::DeviceBuffer final_norm(2 * H), hidden(2 * H), h(2 * I), idx(4), logits(2 * V), sidx(8);
+    mq4::DeviceBuffer final_norm(2 * H), hidden(2 * H), hidden2(2 * H), h(2 * I), idx(4), logits(2 * V), sidx(8);
     if (fill(final_norm.as<uint16_t>(), H, 2001, 0.1, 0.02, st)) return 3;
     if (fill(hidden.as<uint16_t>(), H, 3000, 0.0, 1.0, st)) return 3;
-    for (int l = 0; l < LAYERS; ++l)
+    if (fill(hidden2.as<uint16_t>(), H, 3000, 0.0, 1.0, st)) return 3;
+    mq4::MlpResidual mlp(1, H, I);
+    for (int l = 0; l < LAYERS; ++l) {
         CHECK(mq4::mlp_forward_residual(hidden.as<uint16_t>(), 1, norms[l].as<uint16_t>(), 1e-6f, layers[l],
                                         h.as<uint16_t>(), st));
+        CHECK(mlp(hidden2.as<uint16_t>(), 1, norms[l].as<uint16_t>(), 1e-6f, layers[l], st));   // one call
+    }
     mq4::GreedyLmHead head(1, V);
     CHECK(head(hidden.as<uint16_t>(), 1, final_norm.as<uint16_t>(), 1e-6f, lmq.value(), idx.as<uint32_t>(),
                logits.as<uint16_t>(), st));
@@ -89,12 +93,14 @@ int main(int argc, char** argv) {
     uint32_t stok[2] = {0, 0};
     if (hipMemcpy(stok, sidx.get(), 8, hipMemcpyDeviceToHost) != hipSuccess) return 4;
     uint32_t tok = 0;
-    std::vector<uint16_t> hid(H);
+    std::vector<uint16_t> hid(H), hid2(H);
     if (hipMemcpy(&tok, idx.get(), 4, hipMemcpyDeviceToHost) != hipSuccess) return 4;
     if (hipMemcpy(hid.data(), hidden.get(), 2 * H, hipMemcpyDeviceToHost) != hipSuccess) return 4;
+    if (hipMemcpy(hid2.data(), hidden2.get(), 2 * H, hipMemcpyDeviceToHost) != hipSuccess) return 4;
     std::printf("token %u\nhidden", tok);
     for (int64_t i = 0; i < H; ++i) std::printf(" %u", hid[i]);
     std::printf("\nsampled %u greedy %u\n", stok[0], stok[1]);
+    std::printf("mlp_residual_same %d\n", hid == hid2 ? 1 : 0);
     (void)hipStreamDestroy(st);
     return 0;
 }

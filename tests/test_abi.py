@@ -213,3 +213,29 @@ def test_noalloc_lm_head_host_validation(mq4):
     assert f(fake(A16), 33, 2048, fake(A16), fake(A16), fake(A16), 1000, fake(A16), None, S) == UNSUPPORTED
     assert "32" in last_error(mq4)
     assert f(fake(A16), 0, 2048, fake(A16), fake(A16), fake(A16), 1000, fake(A16), None, S) == INVALID
+
+
+def test_mlp_residual_workspace_and_validation(mq4):
+    """mq4_mlp_workspace_size: h [M, N] bf16, plus from 33 rows on the paired
+    x [M, K] and the group sums of x and h, each section 256-byte aligned; the
+    entry rejects a missing, small or misaligned workspace (and bad shapes)
+    before enqueueing anything."""
+    L = mq4.lib()
+    up = lambda v: (v + 255) // 256 * 256
+    assert L.mq4_mlp_workspace_size(0, 2048, 6144) == 0
+    assert L.mq4_mlp_workspace_size(4, 2048, 6144) == up(4 * 6144 * 2)
+    M, K, N = 2048, 2048, 6144
+    assert L.mq4_mlp_workspace_size(M, K, N) == up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) + up(M * N // 64 * 4)
+    need = L.mq4_mlp_workspace_size(40, 2048, 6144)
+    w = [fake(A16)] * 9
+    call = lambda ws, nb, **kw: L.mq4_mlp_residual(kw.get("x", fake(A16)), kw.get("M", 40), kw.get("K", 2048),
+                                                   fake(A16), ctypes.c_float(1e-6), *w, kw.get("N", 6144), ws, nb,
+                                                   kw.get("y", fake(A16)), S)
+    assert call(None, need) == WORKSPACE
+    assert call(fake(A16), need - 1) == WORKSPACE
+    assert "workspace" in last_error(mq4)
+    assert call(fake(A16 + 16), need) == WORKSPACE
+    assert call(fake(A16), need, K=100) == INVALID
+    assert call(fake(A16), need, M=0) == INVALID
+    assert call(fake(A16), need, y=None) == INVALID
+    assert call(fake(A16), need, x=fake(A16 + 2)) == ALIGN

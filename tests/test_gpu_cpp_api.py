@@ -46,3 +46,5 @@ def test_cpp_demo_matches_python_binding(mq4, O, dev):
     assert int(words[3]) == tok
     want = mq4.sample_token(logits, temperature=0.8, top_k=50, seed=5)
     assert int(words[1]) == int(want.cpu()[0])
+    # mq4::MlpResidual (one mq4_mlp_residual call per layer) gave the same hidden state
+    assert lines[3] == "mlp_residual_same 1"

@@ -189,3 +189,55 @@ def test_gemm_epilogues_at_prefill_m(mq4, O, dev):
     assert np.array_equal(to_host_u16(yr), O.add_bf16(to_host_u16(res), O.f32_to_bf16(yd32.cpu().numpy())))
     ref64d, _ = O.qmm_f64(to_host_u16(h)[rows], *dh)
     check_f32(yd32.cpu().numpy()[rows], ref64d, "prefill down fp32")
+
+
+@pytest.mark.parametrize("M,K,N", [(1960, 2048, 6144), (200, 2048, 6144), (40, 512, 1024), (5, 2048, 6144),
+                                   (70, 640, 1280)])
+def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
+    """mq4_mlp_residual: x + mlp_forward(rms_norm(x)) in one call
+    (src/model/marlin.cpp:141-142).  From 33 rows on with K, N multiples of 512
+    it runs the GEMM on operands stored in the matrix cores' order with their
+    group sums ((1960, 2048, 6144), (200, ...), (40, 512, 1024)); (5, ...) takes
+    the GEMV kernels and (70, 640, 1280) the separate GEMM kernels.
+    * Against the separate entries (mq4_rmsnorm_gate_up_silu +
+      mq4_qmm_residual, each pinned to the oracle): the same normalized
+      operand and bf16 h, fp32 sums in another order, so >= 98% of outputs
+      bit-identical and rms of the difference of the MLP parts <= 1e-2 of rms;
+      on the GEMV path bit for bit.
+    * Against the oracle's chain (rms_norm, gate/up, bf16 SwiGLU, fp64 down,
+      bf16 residual add) on sampled rows: rms(err) <= 1e-2 x rms of the
+      oracle's MLP output."""
+    print(f"mlp_residual M={M} K={K} N={N}", flush=True)
+    ws = [make(mq4, O, *((N, K) if p < 2 else (K, N)), 1100 + p, dev) for p in range(3)]
+    w = mq4.MLPWeights(*[mq4.QuantizedTensor(*d) for d, _ in ws])
+    x = mq4.fill_normal_bf16((M, K), mq4.STREAM_PREFILL, 0.0, 1.0, device=dev)
+    nw = mq4.fill_normal_bf16((K,), mq4.stream_id_layer_norm(0), 0.1, 0.02, device=dev)
+    y = mq4.mlp_residual(x, w, nw, 1e-6)
+    h = mq4.mlp_gate_up_silu(x, w.gate_proj, w.up_proj, norm_weight=nw, eps=1e-6)
+    ys = mq4.qmatmul_residual(h, w.down_proj, x)
+    yi = x.clone()
+    mq4.mlp_residual(yi, w, nw, 1e-6, out=yi)                      # in place
+    torch.cuda.synchronize()
+    got, sep, xh = to_host_u16(y), to_host_u16(ys), to_host_u16(x)
+    assert np.array_equal(to_host_u16(yi), got)
+    same = float(np.mean(got == sep))
+    xf = O.bf16_to_f32(xh).astype(np.float64)
+    dm = (O.bf16_to_f32(got) - O.bf16_to_f32(sep)).astype(np.float64)
+    ms = O.bf16_to_f32(sep).astype(np.float64) - xf
+    rel = float(np.sqrt(np.mean(dm * dm) / np.mean(ms * ms)))
+    print(f"vs separate entries: identical {same:.5f}, rms(diff)/rms(mlp) {rel:.2e}")
+    if M < 33:
+        assert np.array_equal(got, sep)
+    assert same >= 0.98 and rel <= TOL
+    rows = sampled_rows(M) if M > 64 else np.arange(M)
+    rows = rows[(rows >= 0) & (rows < M)]
+    xs = xh[rows]
+    n = O.rmsnorm_1pw(xs, to_host_u16(nw), 1e-6)
+    (g, gh), (u, uh), (d, dh) = ws
+    _, _, _, yb = O.mlp_forward(n, gh, uh, dh)
+    ref = O.add_bf16(xs, yb)
+    err = (O.bf16_to_f32(got[rows]) - O.bf16_to_f32(ref)).astype(np.float64)
+    mo = O.bf16_to_f32(yb).astype(np.float64)
+    rel_o = float(np.sqrt(np.mean(err * err) / np.mean(mo * mo)))
+    print(f"vs oracle chain: rms(err)/rms(mlp) {rel_o:.2e}")
+    assert rel_o <= TOL
