@@ -48,6 +48,7 @@
 
 #include "mq4_device.h"
 #include "mq4_gemm.h"
+#include "mq4_gemv.h"
 #include "mq4_host.h"
 
 namespace mq4 {
@@ -329,9 +330,9 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
     __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
 }
 
-template <int WM, int WN, bool PRE>
+template <int WM, int WN, bool PRE, int TJ>
 struct Stage {
-    static constexpr int BM = 64 * WM, BNW = 64 * WN;
+    static constexpr int BM = 64 * WM, BNW = 32 * TJ * WN;
     uint4 a[BM * 8];                      // [row][chunk ^ ((row >> 1) & 7)]
     uint4 b[2 * BNW];                     // [k-half][weight row]
     uint32_t sb[2][BNW];                  // scales, biases: groups (g & ~1, g | 1)
@@ -343,23 +344,32 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // v_perm_b32 selectors: (lo half of x, lo half of z) and (hi of x, hi of z)
 constexpr uint32_t kPermLo = 0x05040100u, kPermHi = 0x07060302u;
 
-template <int EPI, int WM, int WN, int S, bool PRE>
+template <int EPI, int WM, int WN, int S, bool PRE, int TJ>
 __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p) {
 #pragma clang fp contract(off)
     constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
+    // TJ 32-column weight tiles per wave (2: 64 x 64 outputs; 1: 64 x 32,
+    // twice the waves for a product too small to give every SIMD two; the
+    // fused SwiGLU pairs gate and up tiles, so it takes 2)
+    static_assert(TJ == 2 || (TJ == 1 && NMAT == 1), "wave tile");
     constexpr int NW = WM * WN;
-    constexpr int TBM = 64 * WM, BNW = 64 * WN, BN = BNW / NMAT;
+    constexpr int TBM = 64 * WM, BNW = 32 * TJ * WN, BN = BNW / NMAT;
     constexpr int A_I = TBM * 8 / (64 * NW);            // activation DMA instructions per wave and group
-    constexpr int B_I = 2 * BNW / (64 * NW);            // weight
-    constexpr int SB_I = 2 * BNW / (64 * NW);           // scale/bias
+    // weight and scale/bias tiles: B_TOT instructions per block, issued by the
+    // first waves (with S = 2 every step waits for all of a wave's DMA, so
+    // the per-wave counts need not match)
+    constexpr int B_TOT = 2 * BNW / 64;
+    constexpr int B_I = (B_TOT + NW - 1) / NW;          // weight
+    constexpr int SB_I = B_I;                           // scale/bias
+    static_assert(B_TOT % NW == 0 || S == 2, "uneven DMA split needs the 2-stage ring");
     // PRE: the rows' group sums travel with the tile, 64 rows per DMA
     // instruction, issued by the first TBM / 64 waves (with S = 2 every step
     // waits for all of a wave's DMA, so the counts need not match)
     constexpr int X_I = PRE ? 1 : 0;
     static_assert(!PRE || (S == 2 && TBM / 64 <= NW), "group-sum DMA");
     constexpr int kDmaPerWave = A_I + B_I + SB_I + X_I;
-    static_assert(A_I * 64 * NW == TBM * 8 && B_I * 64 * NW == 2 * BNW, "DMA split");
-    typedef Stage<WM, WN, PRE> St;
+    static_assert(A_I * 64 * NW == TBM * 8, "DMA split");
+    typedef Stage<WM, WN, PRE, TJ> St;
     static_assert(S == 2 || S == 3, "ring stages");
     static_assert((size_t)S * sizeof(St) <= 65536, "LDS DMA targets must lie in the first 64 KiB");
     typedef typename std::conditional<S == 3, St, char>::type St2;   // no third stage with S = 2
@@ -413,7 +423,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
     uint32_t boff[B_I];
 #pragma unroll
     for (int t = 0; t < B_I; ++t) {
-        const int q0 = (wave * B_I + t) * 64, half = q0 / BNW, r0 = q0 % BNW;
+        const int q0 = ((wave * B_I + t) % B_TOT) * 64, half = q0 / BNW, r0 = q0 % BNW;
         bbase[t] = reinterpret_cast<const char*>(mat_of(r0).wq) + half * 16;
         boff[t] = (uint32_t)((int64_t)wrow_of(r0 + lane) * (K / 2));
     }
@@ -421,7 +431,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
     uint32_t sboff[SB_I];
 #pragma unroll
     for (int t = 0; t < SB_I; ++t) {
-        const int u0 = (wave * SB_I + t) * 64, sel = u0 / BNW, r0 = u0 % BNW;
+        const int u0 = ((wave * SB_I + t) % B_TOT) * 64, sel = u0 / BNW, r0 = u0 % BNW;
         sbbase[t] = reinterpret_cast<const char*>(sel ? mat_of(r0).b : mat_of(r0).s);
         sboff[t] = (uint32_t)((int64_t)wrow_of(r0 + lane) * G * 2);
     }
@@ -442,46 +452,50 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
             lds_dma16(xbase + g * 128 + aoff[t], &st.a[(wave * A_I + t) * 64]);
 #pragma unroll
         for (int t = 0; t < B_I; ++t)
-            lds_dma16(bbase[t] + g * 32 + boff[t], &st.b[(wave * B_I + t) * 64]);
+            if (B_TOT % NW == 0 || wave * B_I + t < B_TOT)
+                lds_dma16(bbase[t] + g * 32 + boff[t], &st.b[(wave * B_I + t) * 64]);
 #pragma unroll
         for (int t = 0; t < SB_I; ++t)
-            lds_dma4(sbbase[t] + (g & ~1) * 2 + sboff[t], &st.sb[0][(wave * SB_I + t) * 64]);
+            if (B_TOT % NW == 0 || wave * SB_I + t < B_TOT)
+                lds_dma4(sbbase[t] + (g & ~1) * 2 + sboff[t], &st.sb[0][(wave * SB_I + t) * 64]);
     };
 
     // ---- compute roles: weight row of tile j for this lane ----
-    int wr[2];
+    int wr[TJ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wn * 32 + col : wn * 64 + j * 32 + col;
+    for (int j = 0; j < TJ; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wn * 32 + col : wn * 32 * TJ + j * 32 + col;
     const uint32_t ONES = 0x3f803f80u;        // bf16 pair (1, 1)
     uint32_t nib_mask, nib_exp;               // the nibble-pair constants, set up once
     asm("s_mov_b32 %0, 0x000f000f" : "=s"(nib_mask));
     asm("v_mov_b32 %0, 0x43004300" : "=v"(nib_exp));
 
-    f32x16_t acc[2][2];
+    f32x16_t acc[2][TJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
     const f32x16_t zero = acc[0][0];
-    float xprev[2] = {0.0f, 0.0f}, cprev[2] = {0.0f, 0.0f};
+    float xprev[2] = {0.0f, 0.0f}, cprev[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) cprev[j] = 0.0f;
 
     auto compute = [&](int g, const St& st) {
-        uint4 bw[2];
-        float s[2], c[2];
+        uint4 bw[TJ];
+        float s[TJ], c[TJ];
         const int sh16 = (g & 1) * 16;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TJ; ++j) {
             bw[j] = st.b[h * BNW + wr[j]];
             s[j] = bf16_to_f32((st.sb[0][wr[j]] >> sh16) & 0xffffu);
             c[j] = affine_c(s[j], (st.sb[1][wr[j]] >> sh16) & 0xffffu);
         }
-        f32x16_t D[2][2];
+        f32x16_t D[2][TJ];
         float xs[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf16x8_t a[2], b[2];
+            bf16x8_t a[2], b[TJ];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int r = wm * 64 + i * 32 + col, ch = 4 * h + ks;
@@ -499,11 +513,11 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = weight_operand_k(word_of(bw[j], ks), nib_mask, nib_exp);
+            for (int j = 0; j < TJ; ++j) b[j] = weight_operand_k(word_of(bw[j], ks), nib_mask, nib_exp);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TJ; ++j)
                     D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], ks == 0 ? zero : D[i][j], 0, 0, 0);
         }
         mfma_result_pad();
@@ -517,7 +531,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < TJ; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(s[j], D[i][j][e], acc[i][j][e]);
         // ... and + (b - 128 s) X on the fp32 MFMA, two groups per instruction:
@@ -526,13 +540,13 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
 #pragma unroll
             for (int i = 0; i < 2; ++i) xprev[i] = X[i];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) cprev[j] = c[j];
+            for (int j = 0; j < TJ; ++j) cprev[j] = c[j];
         } else {
             const bool solo = (g & 1) == 0;          // the last group of an odd count
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < TJ; ++j) {
                     const float xa = h ? (solo ? 0.0f : X[i]) : (solo ? X[i] : xprev[i]);
                     const float cb = h ? (solo ? 0.0f : c[j]) : (solo ? c[j] : cprev[j]);
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, cb, acc[i][j], 0, 0, 0);
@@ -584,8 +598,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
-            const int cn = NMAT == 2 ? n0 + wn * 32 + col : n0 + wn * 64 + j * 32 + col;
+        for (int j = 0; j < (NMAT == 2 ? 1 : TJ); ++j) {
+            const int cn = NMAT == 2 ? n0 + wn * 32 + col : n0 + wn * 32 * TJ + j * 32 + col;
             const int cw = paired_out ? ((cn & ~7) | (2 * (cn & 3) + ((cn >> 2) & 1))) : cn;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -632,16 +646,16 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void q4_gemm_dma_kernel(GemmArgs p
     }
 }
 
-// Blocks of the (WM, WN) layout for an M x N product.
-template <int EPI, int WM, int WN>
+// Blocks of the (WM, WN, TJ) layout for an M x N product.
+template <int EPI, int WM, int WN, int TJ>
 unsigned blocks_of(int M, int N) {
-    constexpr int BN = 64 * WN / (EPI == GEMM_SWIGLU ? 2 : 1);
+    constexpr int BN = 32 * TJ * WN / (EPI == GEMM_SWIGLU ? 2 : 1);
     return (unsigned)(((N + BN - 1) / BN) * ((M + 64 * WM - 1) / (64 * WM)));
 }
 
-template <int EPI, int WM, int WN, int S, bool PRE>
+template <int EPI, int WM, int WN, int S, bool PRE, int TJ>
 void launch_dma(const GemmArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((q4_gemm_dma_kernel<EPI, WM, WN, S, PRE>), dim3(blocks_of<EPI, WM, WN>(a.M, a.N)),
+    hipLaunchKernelGGL((q4_gemm_dma_kernel<EPI, WM, WN, S, PRE, TJ>), dim3(blocks_of<EPI, WM, WN, TJ>(a.M, a.N)),
                        dim3(64 * WM * WN), 0, st, a);
 }
 
@@ -651,8 +665,22 @@ void launch_dma(const GemmArgs& a, hipStream_t st) {
 // down (N = 2048) products, with the least LDS (41 KB, so two blocks per CU).
 template <int EPI>
 void launch_dma_auto(const GemmArgs& a, hipStream_t st) {
-    if (a.xsum) launch_dma<EPI, 2, 2, 2, true>(a, st);
-    else launch_dma<EPI, 2, 2, 2, false>(a, st);
+    if (a.xsum) {
+        // paired operands: no activation work per wave, so 64 x 32 wave tiles
+        // cost the same VALU per MFMA as 64 x 64; when 64 x 64 would leave one
+        // block per CU (the down product at M ~ 2,000: 256 blocks), they
+        // double the blocks (126 VGPRs, 4 waves per SIMD): 243-248 against
+        // 257-258 us for the whole MLP half at M = 2048
+        if constexpr (EPI != GEMM_SWIGLU) {
+            if (blocks_of<EPI, 2, 2, 2>(a.M, a.N) <= (unsigned)num_cus()) {
+                launch_dma<EPI, 2, 2, 2, true, 1>(a, st);
+                return;
+            }
+        }
+        launch_dma<EPI, 2, 2, 2, true, 2>(a, st);
+    } else {
+        launch_dma<EPI, 2, 2, 2, false, 2>(a, st);
+    }
 }
 
 }  // namespace dma
