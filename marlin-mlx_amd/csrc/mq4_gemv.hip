@@ -784,7 +784,7 @@ static MlpWs mlp_ws_layout(void* base, int64_t M, int64_t K, int64_t N) {
 static bool mlp_paired_ok(int64_t M, int64_t K, int64_t N, const QMat& g, const QMat& u, const QMat& d) {
     auto a4 = [](const QMat& q) { return aligned(q.s, 4) && aligned(q.b, 4); };
     return M >= kGemmMinM && K % 512 == 0 && N % 512 == 0 && a4(g) && a4(u) && a4(d) &&
-           M * N * 2 <= 0xFFFFFFFFLL && N * K / 2 <= 0xFFFFFFFFLL;
+           M * K * 2 <= 0xFFFFFFFFLL && M * N * 2 <= 0xFFFFFFFFLL && N * K / 2 <= 0xFFFFFFFFLL;
 }
 
 }  // namespace mq4
