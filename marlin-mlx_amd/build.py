@@ -48,13 +48,45 @@ EXTRA_FLAGS = {
     "mq4_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
+# Sources whose kernels wait for their LDS DMA with exact vmcnt counts: that
+# count assumes no other vector memory traffic in the loop, and register
+# spills to scratch are vector memory operations (a spilling build waits too
+# little and reads stages before their DMA has landed).  The build fails if
+# any kernel in them uses scratch.
+NO_SCRATCH = {"mq4_gemm.hip", "mq4_decode.hip"}
+
+
+def _scratch_users(remarks: str) -> list[tuple[str, int]]:
+    """(kernel, bytes per lane) for every function the resource-usage remarks
+    report with a nonzero ScratchSize."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name: " in line:
+            name = line.split("Function Name: ", 1)[1].split()[0]
+        elif "ScratchSize [bytes/lane]: " in line and name is not None:
+            n = int(line.split("ScratchSize [bytes/lane]: ", 1)[1].split()[0])
+            if n > 0:
+                out.append((name, n))
+    return out
+
 
 def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
+    base = os.path.basename(src)
+    obj = os.path.join(BUILD, base + ".o")
+    check = base in NO_SCRATCH
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(base, []),
+           *(["-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"] if check else []),
+           "-c", src, "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass does not know the packed-fp32 feature; that notice is harmless.
-    err = "\n".join(l for l in p.stderr.splitlines() if "packed-fp32-ops" not in l)
+    lines = [l for l in p.stderr.splitlines() if "packed-fp32-ops" not in l]
+    if check:
+        spills = _scratch_users("\n".join(lines))
+        lines = [l for l in lines if "kernel-resource-usage" not in l]
+        if spills and p.returncode == 0:
+            raise RuntimeError(f"{base}: kernels use scratch memory, which breaks their exact vmcnt waits "
+                               f"for LDS DMA: " + ", ".join(f"{k} ({n} B/lane)" for k, n in spills))
+    err = "\n".join(lines)
     if p.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{err}")
     if err.strip():
