@@ -285,6 +285,8 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     scales = _need(scales, torch.bfloat16, "scales")
     biases = _need(biases, torch.bfloat16, "biases")
     M, K, y = _mk(x, N)
+    if M == 0:                      # no rows: an empty result, as mx::quantized_matmul gives
+        return y
     _check(lib().mq4_qmm(_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N, int(transpose),
                          group_size, bits, _ptr(y), _stream(x.device)))
     return y
@@ -301,6 +303,8 @@ def quantized_matmul_f32(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     K = x.shape[-1]
     M = x.numel() // K
     y = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=x.device)
+    if M == 0:
+        return y
     _check(lib().mq4_qmm_f32(_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N, _ptr(y),
                              _stream(x.device)))
     return y
@@ -314,6 +318,8 @@ def argmax(logits: torch.Tensor, axis: int = -1) -> torch.Tensor:
     N = logits.shape[-1]
     M = logits.numel() // N
     idx = torch.empty(logits.shape[:-1], dtype=torch.int32, device=logits.device)
+    if M == 0:
+        return idx
     L = lib()
     ws_bytes = L.mq4_argmax_workspace_size(M, N)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=logits.device)
@@ -403,6 +409,8 @@ def mlp_gate_up_silu(x: torch.Tensor, gate: QuantizedTensor, up: QuantizedTensor
         _check_vector(fn, norm_weight, Kx, "norm_weight")
     x = _need(x, torch.bfloat16, "x")
     M, K, h = _mk(x, N)
+    if M == 0:
+        return h
     g = (_ptr(gate.weight), _ptr(gate.scales), _ptr(gate.biases))
     u = (_ptr(up.weight), _ptr(up.scales), _ptr(up.biases))
     if norm_weight is None:
@@ -434,6 +442,8 @@ def qmatmul_residual(x: torch.Tensor, w: QuantizedTensor, residual: torch.Tensor
     x = _need(x, torch.bfloat16, "x")
     residual = _need(residual, torch.bfloat16, "residual")
     y = out if out is not None else torch.empty_like(residual)
+    if M == 0:
+        return y
     _check(lib().mq4_qmm_residual(_ptr(x), M, K, _ptr(w.weight), _ptr(w.scales), _ptr(w.biases), N,
                                   _ptr(residual), _ptr(y), _stream(x.device)))
     return y
@@ -477,6 +487,8 @@ def mlp_residual(x: torch.Tensor, w: MLPWeights, norm_weight: torch.Tensor, eps:
     y = torch.empty_like(x) if out is None else _need(out, torch.bfloat16, "out")
     if y.shape != x.shape:
         raise ValueError(f"{fn}: out has shape {tuple(y.shape)}, x {tuple(x.shape)}")
+    if M == 0:
+        return y
     L = lib()
     ws_bytes = L.mq4_mlp_workspace_size(M, K, N)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
@@ -508,6 +520,8 @@ def lm_head_argmax(hidden: torch.Tensor, w: QuantizedTensor, return_logits: bool
     idx = torch.empty(hidden.shape[:-1], dtype=torch.int32, device=hidden.device)
     logits = (torch.empty((*hidden.shape[:-1], N), dtype=torch.bfloat16, device=hidden.device)
               if return_logits else None)
+    if M == 0:
+        return (idx, logits) if return_logits else idx
     L = lib()
     ws_bytes = L.mq4_lm_head_argmax_workspace_size(M, N)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=hidden.device)
@@ -589,6 +603,8 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
     weight = _need(weight, torch.bfloat16, "weight")
     K = x.shape[-1]
     out = torch.empty_like(x)
+    if out.numel() == 0:
+        return out
     _check(lib().mq4_rms_norm(_ptr(x), x.numel() // K, K, _ptr(weight), eps, _ptr(out),
                               _stream(x.device)))
     return out

@@ -320,6 +320,33 @@ def test_qmm_batched_leading_dims(mq4, O, dev):
     check_close(O, to_host_u16(y).reshape(S, N), ref, "qmm [1,S,K]")
 
 
+def test_empty_batches(mq4, O, dev):
+    """Zero activation rows give empty results of the right shapes (as
+    mx::quantized_matmul, argmax and rms_norm do on empty inputs) without
+    reaching the C ABI, which rejects M = 0."""
+    N, K, I = 256, 512, 1024
+    w, _ = gen_weight(mq4, O, 1234, N, K)
+    g, _ = gen_weight(mq4, O, 1235, I, K)
+    u, _ = gen_weight(mq4, O, 1236, I, K)
+    d, _ = gen_weight(mq4, O, 1237, K, I)
+    qw, qg, qu, qd = (mq4.quantize_weight(t) for t in (w, g, u, d))
+    nw = torch.zeros(K, dtype=torch.bfloat16, device=dev)
+    for lead in ((0,), (1, 0)):
+        x = torch.empty((*lead, K), dtype=torch.bfloat16, device=dev)
+        assert mq4.qmatmul(x, qw).shape == (*lead, N)
+        assert mq4.quantized_matmul_f32(x, qw.weight, qw.scales, qw.biases).shape == (*lead, N)
+        assert mq4.mlp_gate_up_silu(x, qg, qu).shape == (*lead, I)
+        assert mq4.mlp_gate_up_silu(x, qg, qu, norm_weight=nw).shape == (*lead, I)
+        h = torch.empty((*lead, I), dtype=torch.bfloat16, device=dev)
+        assert mq4.qmatmul_residual(h, qd, x).shape == (*lead, K)
+        assert mq4.mlp_residual(x, mq4.MLPWeights(qg, qu, qd), nw).shape == (*lead, K)
+        assert mq4.rms_norm(x, nw).shape == (*lead, K)
+        idx, logits = mq4.lm_head_argmax(x, qw, return_logits=True)
+        assert idx.shape == lead and logits.shape == (*lead, N)
+        assert mq4.argmax(torch.empty((*lead, N), dtype=torch.bfloat16, device=dev)).shape == lead
+    torch.cuda.synchronize()
+
+
 def check_swiglu(O, got, ref, what):
     """h is bf16(bf16(bf16(sigmoid(g))*g)*u) of bf16-rounded GEMV outputs g, u.
     A 1-ulp difference in the rounding of g or u (when the fp32 sum sits next
