@@ -163,6 +163,7 @@ inline Result<std::vector<QuantizedTensor>> quantize_weights(const std::vector<W
 inline Result<int> qmatmul(const uint16_t* x, int64_t M, const QuantizedTensor& w, uint16_t* y,
                            hipStream_t stream) {
     if (!w.quantized) return Error{MQ4_ERR_UNSUPPORTED, "qmatmul: unquantized weights are outside this library"};
+    if (M == 0) return 0;   // no rows: nothing to compute (the C ABI rejects M = 0)
     const int rc = mq4_qmm(x, M, w.in_features, w.wq(), w.s(), w.b(), w.out_features, 1, w.group_size, w.bits, y,
                            stream);
     if (rc != MQ4_OK) return last_error(rc);
@@ -178,6 +179,7 @@ struct MLPWeights {   // src/model/marlin.h:17-21
 inline Result<int> mlp_forward_residual(uint16_t* hidden, int64_t M, const uint16_t* norm_weight, float eps,
                                         const MLPWeights& w, uint16_t* h, hipStream_t stream) {
     const int64_t K = w.gate_proj.in_features, N = w.gate_proj.out_features;
+    if (M == 0) return 0;
     int rc = norm_weight
                  ? mq4_rmsnorm_gate_up_silu(hidden, M, K, norm_weight, eps, w.gate_proj.wq(), w.gate_proj.s(),
                                             w.gate_proj.b(), w.up_proj.wq(), w.up_proj.s(), w.up_proj.b(), N, h,
@@ -201,6 +203,7 @@ public:
     Result<int> operator()(uint16_t* x, int64_t M, const uint16_t* norm_weight, float eps, const MLPWeights& w,
                            hipStream_t stream) {
         if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "MlpResidual: M exceeds max_rows"};
+        if (M == 0) return 0;
         const int rc = mq4_mlp_residual(x, M, w.gate_proj.in_features, norm_weight, eps, w.gate_proj.wq(),
                                         w.gate_proj.s(), w.gate_proj.b(), w.up_proj.wq(), w.up_proj.s(),
                                         w.up_proj.b(), w.down_proj.wq(), w.down_proj.s(), w.down_proj.b(),
@@ -223,6 +226,7 @@ public:
     Result<int> operator()(const uint16_t* hidden, int64_t M, const uint16_t* final_norm, float eps,
                            const QuantizedTensor& lm, uint32_t* idx, uint16_t* logits, hipStream_t stream) {
         if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "GreedyLmHead: M exceeds max_rows"};
+        if (M == 0) return 0;
         const int rc = final_norm
                            ? mq4_rmsnorm_lm_head_argmax(hidden, M, lm.in_features, final_norm, eps, lm.wq(), lm.s(),
                                                         lm.b(), lm.out_features, idx, logits, ws_.get(), ws_.bytes(),

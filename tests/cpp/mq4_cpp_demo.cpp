@@ -101,6 +101,14 @@ int main(int argc, char** argv) {
     for (int64_t i = 0; i < H; ++i) std::printf(" %u", hid[i]);
     std::printf("\nsampled %u greedy %u\n", stok[0], stok[1]);
     std::printf("mlp_residual_same %d\n", hid == hid2 ? 1 : 0);
+    // zero rows: every mirror returns success without touching its outputs
+    bool empty_ok = mq4::qmatmul(hidden.as<uint16_t>(), 0, lmq.value(), logits.as<uint16_t>(), st).ok() &&
+                    mq4::mlp_forward_residual(hidden.as<uint16_t>(), 0, norms[0].as<uint16_t>(), 1e-6f, layers[0],
+                                              h.as<uint16_t>(), st).ok() &&
+                    mlp(hidden2.as<uint16_t>(), 0, norms[0].as<uint16_t>(), 1e-6f, layers[0], st).ok() &&
+                    head(hidden.as<uint16_t>(), 0, final_norm.as<uint16_t>(), 1e-6f, lmq.value(), idx.as<uint32_t>(),
+                         nullptr, st).ok();
+    std::printf("empty_ok %d\n", empty_ok ? 1 : 0);
     (void)hipStreamDestroy(st);
     return 0;
 }

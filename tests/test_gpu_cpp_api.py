@@ -48,3 +48,4 @@ def test_cpp_demo_matches_python_binding(mq4, O, dev):
     assert int(words[1]) == int(want.cpu()[0])
     # mq4::MlpResidual (one mq4_mlp_residual call per layer) gave the same hidden state
     assert lines[3] == "mlp_residual_same 1"
+    assert lines[4] == "empty_ok 1"
