@@ -47,7 +47,7 @@ constexpr int kNCW = 8;              // compute waves per workgroup
 constexpr int kThreads = 64 * (kNIO + kNCW);
 constexpr int kMaxLayers = 32;
 constexpr int kCopies = 8;           // replicas of the exchange buffers (one per XCD)
-constexpr int kFirstPollSleep = 20;  // s_sleep units (64 clocks) before the first poll round
+constexpr int kFirstPollSleep = 28;  // s_sleep units (64 clocks) before the first poll round
 constexpr int H = 2048;              // hidden size this instance is built for
 constexpr int I = 6144;              // intermediate size
 constexpr int SA = H / 32;           // 16-byte slices per gate/up row (64)
@@ -104,10 +104,12 @@ template <int NW>
 __device__ bool poll_words(const uint64_t* src, uint32_t tag, uint32_t* dst, const Params& p, int lane) {
     constexpr int PER = NW / 64;
     uint64_t w[PER];
-    // The first round is delayed by ~0.5 us: issued right after this
-    // workgroup's own publish it meets the other workgroups' stores still in
-    // flight and takes ~1.5 us to return (and fails), while a round issued
-    // slightly later returns in ~0.6 us with the phase complete.
+    // The first round is delayed by 28 x 64 clocks (~0.75 us): issued right
+    // after this workgroup's own publish it meets the other workgroups'
+    // stores still in flight and takes ~1.5 us to return (and fails), while a
+    // round issued later returns in ~0.6 us with the phase complete.  (Swept
+    // on MI355X: 12-48 units give 207-212 us per step at the ends, 195 us at
+    // 24-32; separate delays for the x and h exchanges gain nothing.)
     __builtin_amdgcn_s_sleep(kFirstPollSleep);
     for (int spins = 0;; ++spins) {
 #pragma unroll
