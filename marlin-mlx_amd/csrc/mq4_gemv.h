@@ -10,7 +10,14 @@
 
 namespace mq4 {
 
-enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3, EPI_STORE_F32 = 4 };
+enum Epilogue {
+    EPI_STORE = 0,
+    EPI_RESIDUAL = 1,
+    EPI_SWIGLU = 2,
+    EPI_ARGMAX = 3,
+    EPI_STORE_F32 = 4,
+    EPI_PARTIAL = 5,   // MFMA GEMV, K split over blockIdx.y: fp32 sum of the block's part to y[part][M][N]
+};
 
 constexpr int kPartialStride = 4096;     // max blocks of an argmax launch
 
@@ -39,6 +46,19 @@ constexpr int kMfmaMaxM = 32;
 // this K / epilogue combination is not provided (the caller then uses the
 // dot2 GEMV).
 int launch_q4_mfma_gemv(const GemvParams& a, int epi, bool norm, hipStream_t st);
+
+// The down product of a small-M MLP with its K range split over two blocks
+// per 16-row tile (each block half the activations, all CUs busy): enqueues
+// the fp32 sums of the two K parts into part [2][M][N] and returns 0, or -1
+// when the product is not one the 12-wave MFMA GEMV would run (64 < K/64 <=
+// 96, M <= kMfmaMaxM).  Each part is the in-block sum of 6 waves in wave
+// order; launch_combine2_residual adds the two parts, which is exactly the
+// 12-wave kernel's reduction, so the result is bit-identical to it.
+int launch_q4_mfma_gemv_split2(const GemvParams& a, float* part, hipStream_t st);
+
+// y = bf16(bf16(res) + round_bf16(part[0] + part[1])) over M x N values (the
+// residual epilogue of the MFMA GEMV applied to the two K parts).
+void launch_combine2_residual(const float* part, int M, int N, const uint16_t* res, uint16_t* y, hipStream_t st);
 
 // idx[m] = argmax of the per-block keys partial[m * kPartialStride + 0 .. count).
 void launch_argmax_finalize(const uint64_t* partial, int count, int M, uint32_t* idx, hipStream_t st);

@@ -748,13 +748,16 @@ namespace mq4 {
 // Workspace: h [M, N] bf16; on the GEMM path h is written in the GEMM's
 // operand order by the SwiGLU epilogue, and the normalized x (by
 // launch_pair_rows) too, both with their fp32 group sums, so neither GEMM
-// forms them per wave.  Sections 256-byte aligned.
+// forms them per wave.  On the MFMA GEMV path (kMfmaMinM <= M < kGemmMinM)
+// part [2, M, K] fp32 holds the two K parts of the split down product.
+// Sections 256-byte aligned.
 struct MlpWs {
     uint16_t* h = nullptr;
     uint16_t* xp = nullptr;
     float* xs = nullptr;
     uint16_t* hp = nullptr;
     float* hs = nullptr;
+    float* part = nullptr;
     size_t bytes = 0;
 };
 
@@ -773,6 +776,8 @@ static MlpWs mlp_ws_layout(void* base, int64_t M, int64_t K, int64_t N) {
         w.xp = reinterpret_cast<uint16_t*>(take((size_t)M * K * 2));
         w.xs = reinterpret_cast<float*>(take((size_t)M * (K / 64) * 4));
         w.hs = reinterpret_cast<float*>(take((size_t)M * (N / 64) * 4));
+    } else if (M >= kMfmaMinM) {
+        w.part = reinterpret_cast<float*>(take((size_t)2 * M * K * 4));
     }
     w.bytes = off;
     return w;
@@ -830,6 +835,13 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
         return rc;
     GemvParams a = params(w.h, M, N, K, D, {nullptr, nullptr, nullptr}, y);
     a.res = x;
+    // from kMfmaMinM rows the down product runs as two K parts per tile (half
+    // the activations per block, all CUs busy), bit-identical to the one-block
+    // product of mq4_qmm_residual
+    if (M >= kMfmaMinM && M < kGemmMinM && launch_q4_mfma_gemv_split2(a, w.part, st) == 0) {
+        launch_combine2_residual(w.part, (int)M, (int)K, x, y, st);
+        return launch_status(what);
+    }
     if (M >= kGemmMinM) {
         run_gemm(a, M, GEMM_RESIDUAL, st);
         return launch_status(what);

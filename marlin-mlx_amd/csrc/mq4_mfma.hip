@@ -90,6 +90,7 @@ __global__ __launch_bounds__(64 * KS) void q4_mfma_gemv_kernel(GemvParams p) {
 #pragma clang fp contract(off)
     static_assert(MT == 1 || MT == 2, "one or two 16-row tiles of activations");
     static_assert(!NORM || XREG, "the fused norm keeps the activations in registers");
+    static_assert(!(NORM && EPI == EPI_PARTIAL), "the norm needs whole rows, not a K part");
     static_assert(GW % 2 == 0, "scales travel two per dword");
     // the group sums X are recomputed per group and round (two MFMAs against
     // ones): the matrix cores have the headroom, while keeping them in
@@ -99,7 +100,9 @@ __global__ __launch_bounds__(64 * KS) void q4_mfma_gemv_kernel(GemvParams p) {
     const int c16 = lane & 15, kq = lane >> 4;
     const int M = p.m_valid, N = p.N, K = p.K;
     const int G = K >> 6;
-    const int g0 = kw * GW;
+    // EPI_PARTIAL: block y of the grid takes waves y * KS .. y * KS + KS - 1
+    // of the K range (a 12-wave product as two blocks of 6)
+    const int g0 = ((EPI == EPI_PARTIAL ? (int)blockIdx.y * KS : 0) + kw) * GW;
     const bool wave_live = g0 < G;                 // wave-uniform: this wave has groups
     const int tiles = (N + 15) >> 4;
     const int rounds = (tiles + (int)gridDim.x - 1) / (int)gridDim.x;   // block-uniform
@@ -305,16 +308,32 @@ __global__ __launch_bounds__(64 * KS) void q4_mfma_gemv_kernel(GemvParams p) {
             }
             __syncthreads();
             if (kw == 0) {
+                // wave order; with 12 waves as two halves, (w0 + .. + w5) +
+                // (w6 + .. + w11), which is what the two blocks of the split
+                // product (EPI_PARTIAL) and their combine compute
+                constexpr int KH = KS == 12 ? 6 : KS;
 #pragma unroll
-                for (int k = 0; k < KS - 1; ++k)
+                for (int t = 0; t < NMAT; ++t)
 #pragma unroll
-                    for (int t = 0; t < NMAT; ++t)
+                    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) {
+                        for (int k = 0; k < KH - 1; ++k) {
                             const f32x4_t o = red[k][t * MT + mt][lane];
 #pragma unroll
                             for (int i = 0; i < 4; ++i) acc[t][mt][i] += o[i];
                         }
+                        if constexpr (KH < KS) {
+                            f32x4_t hi = red[KH - 1][t * MT + mt][lane];
+#pragma unroll
+                            for (int k = KH; k < KS - 1; ++k) {
+                                const f32x4_t o = red[k][t * MT + mt][lane];
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) hi[i] += o[i];
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) acc[t][mt][i] += hi[i];
+                        }
+                    }
             }
             __syncthreads();                           // red is rewritten next round
         }
@@ -331,6 +350,8 @@ __global__ __launch_bounds__(64 * KS) void q4_mfma_gemv_kernel(GemvParams p) {
                     const float v = acc[0][mt][i];
                     if constexpr (EPI == EPI_STORE) {
                         p.y[o] = (uint16_t)f32_to_bf16(v);
+                    } else if constexpr (EPI == EPI_PARTIAL) {
+                        reinterpret_cast<float*>(p.y)[(int64_t)blockIdx.y * M * N + o] = v;
                     } else if constexpr (EPI == EPI_STORE_F32) {
                         reinterpret_cast<float*>(p.y)[o] = v;
                     } else if constexpr (EPI == EPI_RESIDUAL) {
@@ -364,6 +385,17 @@ __global__ __launch_bounds__(64 * KS) void q4_mfma_gemv_kernel(GemvParams p) {
                     if (c16 == 0 && m < M) p.partial[(int64_t)m * kPartialStride + blockIdx.x] = b;
                 }
         }
+    }
+}
+
+// y = bf16(bf16(res) + round_bf16(part0 + part1)): the residual epilogue on the
+// two K parts of the split product.
+__global__ __launch_bounds__(256) void combine2_residual_kernel(const float* part, int64_t n, const uint16_t* res,
+                                                               uint16_t* y) {
+#pragma clang fp contract(off)
+    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < n; o += (int64_t)gridDim.x * 256) {
+        const float v = part[o] + part[n + o];
+        y[o] = (uint16_t)f32_to_bf16(bf16_to_f32(res[o]) + round_bf16(v));
     }
 }
 
@@ -465,6 +497,46 @@ int dispatch(const GemvParams& a, hipStream_t st) {
 }
 
 }  // namespace
+
+namespace {
+
+template <int MT, bool XREG, bool SBV>
+void launch_split2(const GemvParams& a, int tiles, hipStream_t st) {
+    static int per_cu = 0;
+    auto* k = mf::q4_mfma_gemv_kernel<MT, 8, 6, 1, EPI_PARTIAL, false, XREG, false, SBV>;
+    // two blocks (K parts) per tile; the grid stays within what the GPU holds at once
+    int grid = resident_per_cu<6>(reinterpret_cast<const void*>(k), per_cu) * num_cus() / 2;
+    if (grid < 1) grid = 1;
+    if (grid > tiles) grid = tiles;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid, 2), dim3(64 * 6), 0, st, a);
+}
+
+}  // namespace
+
+int launch_q4_mfma_gemv_split2(const GemvParams& a, float* part, hipStream_t st) {
+    const int G = a.K / 64;
+    // exactly the products the non-split dispatch runs on 12 waves of 8 groups
+    if (a.m_valid < 1 || a.m_valid > kMfmaMaxM || a.K % 64 != 0 || G <= 64 || G > 96 || !part) return -1;
+    GemvParams b = a;
+    b.y = reinterpret_cast<uint16_t*>(part);
+    const int tiles = (a.N + 15) / 16;
+    const bool sbv = G % 8 == 0 && aligned(a.A.s, 16) && aligned(a.A.b, 16);
+    if (a.m_valid <= 16) {
+        if (sbv) launch_split2<1, true, true>(b, tiles, st);
+        else launch_split2<1, true, false>(b, tiles, st);
+    } else {
+        if (sbv) launch_split2<2, false, true>(b, tiles, st);
+        else launch_split2<2, false, false>(b, tiles, st);
+    }
+    return 0;
+}
+
+void launch_combine2_residual(const float* part, int M, int N, const uint16_t* res, uint16_t* y, hipStream_t st) {
+    const int64_t n = (int64_t)M * N;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 2048) blocks = 2048;
+    hipLaunchKernelGGL(mf::combine2_residual_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part, n, res, y);
+}
 
 int launch_q4_mfma_gemv(const GemvParams& a, int epi, bool norm, hipStream_t st) {
     if (a.m_valid < 1 || a.m_valid > kMfmaMaxM) return -1;

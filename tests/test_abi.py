@@ -216,14 +216,17 @@ def test_noalloc_lm_head_host_validation(mq4):
 
 
 def test_mlp_residual_workspace_and_validation(mq4):
-    """mq4_mlp_workspace_size: h [M, N] bf16, plus from 33 rows on the paired
-    x [M, K] and the group sums of x and h, each section 256-byte aligned; the
+    """mq4_mlp_workspace_size: h [M, N] bf16, plus for 5-32 rows the two fp32
+    K parts of the down product [2, M, K], and from 33 rows on the paired x
+    [M, K] and the group sums of x and h, each section 256-byte aligned; the
     entry rejects a missing, small or misaligned workspace (and bad shapes)
     before enqueueing anything."""
     L = mq4.lib()
     up = lambda v: (v + 255) // 256 * 256
     assert L.mq4_mlp_workspace_size(0, 2048, 6144) == 0
     assert L.mq4_mlp_workspace_size(4, 2048, 6144) == up(4 * 6144 * 2)
+    assert L.mq4_mlp_workspace_size(16, 2048, 6144) == up(16 * 6144 * 2) + up(2 * 16 * 2048 * 4)
+    assert L.mq4_mlp_workspace_size(32, 2048, 6144) == up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
     M, K, N = 2048, 2048, 6144
     assert L.mq4_mlp_workspace_size(M, K, N) == up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) + up(M * N // 64 * 4)
     need = L.mq4_mlp_workspace_size(40, 2048, 6144)
