@@ -176,10 +176,13 @@ int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
  * bit for bit).  From M = 33 rows on (K and N multiples of 512, scale and
  * bias rows 4-byte aligned) it runs the MFMA GEMM on activations stored in
  * the matrix cores' operand order with their group sums: a pre-pass writes
- * the normalized x so, the SwiGLU epilogue writes h so.  workspace: at least
- * mq4_mlp_workspace_size(M, K, N) bytes, 256-byte aligned, no
- * initialisation; calls that overlap in time need separate workspaces.  y
- * may equal x (in place). */
+ * the normalized x so, the SwiGLU epilogue writes h so.  From 5 to 32 rows
+ * (with 64 < N / 64 <= 96) the down product runs as two halves of K per
+ * 16-row tile on different workgroups.  Their fp32 sums go to the workspace
+ * and a combine pass adds them with the residual, bit for bit what
+ * mq4_qmm_residual gives.  workspace: at least mq4_mlp_workspace_size(M, K,
+ * N) bytes, 256-byte aligned, no initialisation; calls that overlap in time
+ * need separate workspaces.  y may equal x (in place). */
 size_t mq4_mlp_workspace_size(int64_t M, int64_t K, int64_t N);
 int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K,
                      const uint16_t* norm_weight, float eps,
