@@ -20,6 +20,8 @@ At the prefill sizes (M = 1960 / 2048 / 8192) the oracle checks a spread of
 rows; the others are covered by the row-independent kernel (every row runs
 the same code on its own data) and by the small ragged shapes.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -243,3 +245,52 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     rel_o = float(np.sqrt(np.mean(err * err) / np.mean(mo * mo)))
     print(f"vs oracle chain: rms(err)/rms(mlp) {rel_o:.2e}")
     assert rel_o <= TOL
+
+
+@pytest.mark.parametrize("M", [16, 32])
+def test_mlp_residual_split_graph_replay(mq4, O, dev, M):
+    """The one-call MLP at batched-decode sizes (the down product as two K
+    parts per tile plus a combine) captured in a HIP graph: every replay, with
+    eager work and synchronizations between replays, reproduces the eager call
+    bit for bit, as the batched bench replays it."""
+    K, N = 2048, 6144
+    print(f"mlp_residual graph M={M}", flush=True)
+    ws_ = [make(mq4, O, *((N, K) if p < 2 else (K, N)), 1200 + p, dev) for p in range(3)]
+    w = mq4.MLPWeights(*[mq4.QuantizedTensor(*d) for d, _ in ws_])
+    x = mq4.fill_normal_bf16((M, K), mq4.STREAM_PREFILL + 1, 0.0, 1.0, device=dev)
+    nw = mq4.fill_normal_bf16((K,), mq4.stream_id_layer_norm(1), 0.1, 0.02, device=dev)
+    L = mq4.lib()
+    P = ctypes.c_void_p
+    nb = L.mq4_mlp_workspace_size(M, K, N)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    qa = lambda q: (P(q.weight.data_ptr()), P(q.scales.data_ptr()), P(q.biases.data_ptr()))
+
+    def call(st):
+        mq4._check(L.mq4_mlp_residual(P(x.data_ptr()), M, K, P(nw.data_ptr()), 1e-6, *qa(w.gate_proj),
+                                      *qa(w.up_proj), *qa(w.down_proj), N, P(ws.data_ptr()), nb, P(y.data_ptr()),
+                                      st))
+
+    call(P(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    want = to_host_u16(y).copy()
+    ref = to_host_u16(mq4.qmatmul_residual(mq4.mlp_gate_up_silu(x, w.gate_proj, w.up_proj, norm_weight=nw),
+                                           w.down_proj, x))
+    assert np.array_equal(want, ref)                       # same bits as the separate entries
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call(P(s.cuda_stream))
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(P(torch.cuda.current_stream().cuda_stream))
+    for r in range(3):
+        y.fill_(0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host_u16(y), want), f"replay {r}"
+        mq4.qmatmul(x, w.gate_proj)                        # eager work between replays
+        torch.cuda.synchronize()
