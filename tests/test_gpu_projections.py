@@ -1,4 +1,4 @@
-"""Q4 for the model's other projections (SURVEY next item 4): the same entry
+"""Q4 for the model's other projections (the SSM and attention layers): the same entry
 points at the SSM and attention shapes -- in_proj_qkv 6144x2048
 (src/model/gated_deltanet.cpp:108), in_proj_z / out_proj 2048x2048
 (:109), q_proj 4096x2048, k_proj / v_proj 512x2048, o_proj 2048x2048
