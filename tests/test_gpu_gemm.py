@@ -194,15 +194,17 @@ def test_gemm_epilogues_at_prefill_m(mq4, O, dev):
 
 
 @pytest.mark.parametrize("M,K,N", [(1960, 2048, 6144), (200, 2048, 6144), (40, 512, 1024), (5, 2048, 6144),
-                                   (16, 2048, 6144), (32, 2048, 6144), (24, 2048, 4608), (70, 640, 1280)])
+                                   (16, 2048, 6144), (32, 2048, 6144), (24, 2048, 4608), (7, 1024, 5120),
+                                   (23, 2048, 6144), (70, 640, 1280)])
 def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     """mq4_mlp_residual: x + mlp_forward(rms_norm(x)) in one call
     (src/model/marlin.cpp:141-142).  From 33 rows on with K, N multiples of 512
     it runs the GEMM on operands stored in the matrix cores' order with their
     group sums ((1960, 2048, 6144), (200, ...), (40, 512, 1024)); (5, ...),
-    (16, ...), (32, ...) and (24, 2048, 4608) take the MFMA GEMV kernels, the
-    down product as two K parts per tile and a combine (72 groups: the second
-    part partly empty), and (70, 640, 1280) the separate GEMM kernels.
+    (16, ...), (32, ...), (23, ...), (24, 2048, 4608) and (7, 1024, 5120)
+    take the MFMA GEMV kernels, the down product as two K parts per tile and
+    a combine (72 and 80 groups: the second part partly empty), and (70, 640,
+    1280) the separate GEMM kernels.
     * Against the separate entries (mq4_rmsnorm_gate_up_silu +
       mq4_qmm_residual, each pinned to the oracle): the same normalized
       operand and bf16 h, fp32 sums in another order, so >= 98% of outputs
