@@ -182,7 +182,9 @@ int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
  * and a combine pass adds them with the residual, bit for bit what
  * mq4_qmm_residual gives.  workspace: at least mq4_mlp_workspace_size(M, K,
  * N) bytes, 256-byte aligned, no initialisation; calls that overlap in time
- * need separate workspaces.  y may equal x (in place). */
+ * need separate workspaces.  y may equal x (in place).
+ * mq4_mlp_workspace_size(M, K, N) is enough for every call of at most M rows
+ * with the same K and N: it never shrinks as M grows. */
 size_t mq4_mlp_workspace_size(int64_t M, int64_t K, int64_t N);
 int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K,
                      const uint16_t* norm_weight, float eps,

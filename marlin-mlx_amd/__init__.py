@@ -165,7 +165,12 @@ def _check_weight(fn: str, wq: torch.Tensor, scales: torch.Tensor, biases: torch
         raise TypeError(f"{fn}: scales and biases must be bfloat16")
     if wq.dim() != 2:
         raise ValueError(f"{fn}: packed weight must be 2-D [N, K/8], got shape {tuple(wq.shape)}")
-    if group_size <= 0 or bits <= 0 or K % group_size != 0 or (K * bits) % 32 != 0:
+    if group_size != GROUP_SIZE or bits != BITS:
+        # the kernels are built for MLX's group-64, 4-bit layout only; another
+        # format's scales/biases/words would be read past their ends
+        raise NotImplementedError(f"{fn}: only group_size={GROUP_SIZE}, bits={BITS} is implemented "
+                                  f"(got group_size={group_size}, bits={bits})")
+    if K % group_size != 0 or (K * bits) % 32 != 0:
         raise ValueError(f"{fn}: K={K} is not a multiple of group_size={group_size}")
     N = wq.shape[0]
     if wq.shape[1] != K * bits // 32:
@@ -551,6 +556,16 @@ def lm_head_last_row(hidden: torch.Tensor, w: QuantizedTensor, norm_weight: torc
 
 
 _sample_calls = itertools.count()
+_proc_seed: list[int] = []
+
+
+def _process_seed() -> int:
+    """A 64-bit seed drawn once per process from the OS: like MLX's global
+    random key, which is seeded from the clock, every process draws a
+    different sequence."""
+    if not _proc_seed:
+        _proc_seed.append(int.from_bytes(os.urandom(8), "little"))
+    return _proc_seed[0]
 
 
 def sample_token(logits: torch.Tensor, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
@@ -565,8 +580,10 @@ def sample_token(logits: torch.Tensor, temperature: float = 0.0, top_k: int = 0,
     probability mass of the smaller elements before it exceeds top_p), and
     the token is drawn from softmax(scaled) over the unmasked elements.
     seed: the draw is a pure function of (logits, parameters, seed, row);
-    None takes the next value of a per-process counter, so successive calls
-    draw independently, as the reference's global random key does.
+    None takes a per-process random base (drawn once from the OS) plus a
+    per-process call counter, so successive calls and separate processes
+    draw independently, as the reference's clock-seeded global random key
+    does.
     Returns int64 [M] (and the uint8 [M, V] keep mask with return_keep,
     None for the greedy case)."""
     fn = "sample_token"
@@ -581,7 +598,7 @@ def sample_token(logits: torch.Tensor, temperature: float = 0.0, top_k: int = 0,
     rows = _need(logits, torch.bfloat16, "logits").contiguous()
     M, V = rows.shape
     if seed is None:
-        seed = (SEED * 0x9E3779B97F4A7C15 + next(_sample_calls)) & 0xFFFFFFFFFFFFFFFF
+        seed = (_process_seed() + next(_sample_calls)) & 0xFFFFFFFFFFFFFFFF
     idx = torch.empty(M, dtype=torch.int32, device=rows.device)
     keep = None
     if return_keep and temperature > 0.0:

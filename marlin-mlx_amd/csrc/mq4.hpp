@@ -20,6 +20,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <initializer_list>
+#include <random>
 #include <string>
 #include <utility>
 #include <variant>
@@ -174,11 +176,26 @@ struct MLPWeights {   // src/model/marlin.h:17-21
     QuantizedTensor gate_proj, up_proj, down_proj;
 };
 
+// The fused entry points (mq4_mlp_residual, mq4_rmsnorm_gate_up_silu,
+// mq4_qmm_residual, mq4_lm_head_argmax) take no format argument: they read
+// the group-64, 4-bit layout only, so a tensor of another format (a cache
+// file MLX wrote with group 128, say) is rejected here before its buffers
+// reach them.
+inline bool q4_format_ok(const QuantizedTensor& q) { return q.quantized && q.group_size == 64 && q.bits == 4; }
+
+inline Result<int> check_q4(const char* fn, std::initializer_list<const QuantizedTensor*> qs) {
+    for (const QuantizedTensor* q : qs)
+        if (!q4_format_ok(*q))
+            return Error{MQ4_ERR_UNSUPPORTED, std::string(fn) + ": needs group_size=64, bits=4 quantized weights"};
+    return 0;
+}
+
 // hidden = hidden + mlp_forward(rms_norm(hidden, norm_weight)) in two kernels
 // (src/model/marlin.cpp:141-142, 31-35); h is scratch of [M, intermediate].
 inline Result<int> mlp_forward_residual(uint16_t* hidden, int64_t M, const uint16_t* norm_weight, float eps,
                                         const MLPWeights& w, uint16_t* h, hipStream_t stream) {
     const int64_t K = w.gate_proj.in_features, N = w.gate_proj.out_features;
+    if (auto r = check_q4("mlp_forward_residual", {&w.gate_proj, &w.up_proj, &w.down_proj}); !r) return r.error();
     if (M == 0) return 0;
     int rc = norm_weight
                  ? mq4_rmsnorm_gate_up_silu(hidden, M, K, norm_weight, eps, w.gate_proj.wq(), w.gate_proj.s(),
@@ -195,7 +212,9 @@ inline Result<int> mlp_forward_residual(uint16_t* hidden, int64_t M, const uint1
 
 // hidden = hidden + mlp_forward(rms_norm(hidden, norm_weight)) in one call
 // (src/model/marlin.cpp:141-142, 31-35), in place; the workspace holds
-// mq4_mlp_workspace_size(max_rows, hidden size, intermediate size) bytes.
+// mq4_mlp_workspace_size(max_rows, hidden size, intermediate size) bytes,
+// which covers every call of at most max_rows rows (the size never shrinks
+// as the row count grows).
 class MlpResidual {
 public:
     MlpResidual(int64_t max_rows, int64_t hidden, int64_t intermediate)
@@ -203,6 +222,7 @@ public:
     Result<int> operator()(uint16_t* x, int64_t M, const uint16_t* norm_weight, float eps, const MLPWeights& w,
                            hipStream_t stream) {
         if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "MlpResidual: M exceeds max_rows"};
+        if (auto r = check_q4("MlpResidual", {&w.gate_proj, &w.up_proj, &w.down_proj}); !r) return r.error();
         if (M == 0) return 0;
         const int rc = mq4_mlp_residual(x, M, w.gate_proj.in_features, norm_weight, eps, w.gate_proj.wq(),
                                         w.gate_proj.s(), w.gate_proj.b(), w.up_proj.wq(), w.up_proj.s(),
@@ -226,6 +246,7 @@ public:
     Result<int> operator()(const uint16_t* hidden, int64_t M, const uint16_t* final_norm, float eps,
                            const QuantizedTensor& lm, uint32_t* idx, uint16_t* logits, hipStream_t stream) {
         if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "GreedyLmHead: M exceeds max_rows"};
+        if (auto r = check_q4("GreedyLmHead", {&lm}); !r) return r.error();
         if (M == 0) return 0;
         const int rc = final_norm
                            ? mq4_rmsnorm_lm_head_argmax(hidden, M, lm.in_features, final_norm, eps, lm.wq(), lm.s(),
@@ -255,13 +276,24 @@ private:
 
 // The sampling fields of the reference's SamplingConfig
 // (src/core/config.h:60-63); seed drives this library's counter-based
-// generator (the reference's seed field is unused and MLX's global key draws).
+// generator (the reference's seed field is unused and MLX's global key,
+// seeded from the clock, draws).  seed = -1, the reference's default, takes
+// a base drawn once per process from std::random_device, so separate
+// processes draw different sequences, as they do in the reference.
 struct SamplingConfig {
     float temperature = 0.0f;
     float top_p = 1.0f;
     int top_k = 0;
-    uint64_t seed = 0;
+    int64_t seed = -1;
 };
+
+inline uint64_t process_seed() {
+    static const uint64_t s = [] {
+        std::random_device rd;
+        return ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+    }();
+    return s;
+}
 
 // sample_token over bf16 logits [M, vocab] (src/sampling/sampler.cpp:9-39),
 // one token per row.  Each call draws with seed + the number of earlier
@@ -282,7 +314,8 @@ public:
         if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "Sampler: M exceeds max_rows"};
         const size_t need = mq4_sample_workspace_size(M, vocab_);
         if (need > ws_.bytes()) return Error{MQ4_ERR_WORKSPACE, "Sampler: workspace allocation failed"};
-        const int rc = mq4_sample_bf16(logits, M, vocab_, c.temperature, c.top_k, c.top_p, c.seed + calls_++, idx,
+        const uint64_t base = c.seed < 0 ? process_seed() : (uint64_t)c.seed;
+        const int rc = mq4_sample_bf16(logits, M, vocab_, c.temperature, c.top_k, c.top_p, base + calls_++, idx,
                                        keep, need ? ws_.get() : nullptr, need, stream);
         if (rc != MQ4_OK) return last_error(rc);
         return 0;

@@ -71,8 +71,17 @@ public:
     }
 
 private:
+    // A safetensors header nests three levels deep; the limit keeps a crafted
+    // header from exhausting the stack through the recursion below.
+    static constexpr int kMaxDepth = 32;
     const std::string& s_;
     size_t i_ = 0;
+    int depth_ = 0;
+    struct Nest {
+        int& d;
+        explicit Nest(int& d_) : d(++d_) {}
+        ~Nest() { --d; }
+    };
     void ws() {
         while (i_ < s_.size() && std::isspace((unsigned char)s_[i_])) ++i_;
     }
@@ -107,6 +116,8 @@ private:
         return true;
     }
     bool value(Json& v) {
+        const Nest nest(depth_);
+        if (depth_ > kMaxDepth) return false;
         ws();
         if (i_ >= s_.size()) return false;
         const char c = s_[i_];
@@ -259,15 +270,20 @@ inline Result<std::map<std::string, HostTensor>> read_safetensors(const std::str
             return Error{MQ4_ERR_INVALID_ARG, path + ": malformed entry " + name};
         HostTensor t;
         t.dtype = dt->str;
-        int64_t cnt = 1;
+        // element and byte counts without overflow: each dimension is capped
+        // and every product is checked, so no wrapped count can match the
+        // data offsets while the dimensions disagree with the bytes
+        constexpr int64_t kMaxDim = int64_t(1) << 40;
+        int64_t cnt = 1, nbytes = 0;
         for (auto& d : sh->arr) {
-            if (d.kind != Json::NUM || d.num < 0) return Error{MQ4_ERR_INVALID_ARG, path + ": bad shape of " + name};
+            if (d.kind != Json::NUM || d.num < 0 || d.num > kMaxDim || __builtin_mul_overflow(cnt, d.num, &cnt))
+                return Error{MQ4_ERR_INVALID_ARG, path + ": bad shape of " + name};
             t.shape.push_back(d.num);
-            cnt *= d.num;
         }
         const int64_t b = of->arr[0].num, en = of->arr[1].num;
-        if (b < 0 || en < b || (uint64_t)en > data_size || dtype_size(t.dtype) == 0 ||
-            en - b != cnt * dtype_size(t.dtype))
+        if (of->arr[0].kind != Json::NUM || of->arr[1].kind != Json::NUM || b < 0 || en < b ||
+            (uint64_t)en > data_size || dtype_size(t.dtype) == 0 ||
+            __builtin_mul_overflow(cnt, dtype_size(t.dtype), &nbytes) || en - b != nbytes)
             return Error{MQ4_ERR_INVALID_ARG, path + ": data offsets of " + name + " do not match its shape"};
         t.data.assign(data.begin() + b, data.begin() + en);
         out.emplace(name, std::move(t));
@@ -308,16 +324,31 @@ inline Result<int> save_q4_cache(const std::string& path,
                                         {"quantization.bits", std::to_string(bits)}});
 }
 
+// The group size and bit width a cache file records (64 and 4 when absent).
+// MLX also writes group 32 / 128 and 2, 3, 6 or 8 bits; the library's kernels
+// read only the group-64, 4-bit layout, so any other format is refused here,
+// before its buffers could reach an entry point that assumes that layout.
+inline Result<int> q4_cache_format(const std::map<std::string, std::string>& meta, const std::string& path) {
+    auto num = [&](const char* key, int dflt) {
+        auto it = meta.find(key);
+        return it == meta.end() ? dflt : std::atoi(it->second.c_str());
+    };
+    const int gs = num("quantization.group_size", 64), bits = num("quantization.bits", 4);
+    if (gs != 64 || bits != 4)
+        return Error{MQ4_ERR_UNSUPPORTED, path + ": holds group_size=" + std::to_string(gs) + ", bits=" +
+                                              std::to_string(bits) + "; only group_size=64, bits=4 is implemented"};
+    return 0;
+}
+
 // Load every "<name>.weight/.scales/.biases" triple of a cache file to the
-// device (shapes and dtypes checked against the recorded group size and bits).
+// device (shapes and dtypes checked against the group-64, 4-bit layout).
 inline Result<std::map<std::string, QuantizedTensor>> load_q4_cache(const std::string& path) {
     std::map<std::string, std::string> meta;
     auto rr = read_safetensors(path, &meta);
     if (!rr) return rr.error();
     auto& t = rr.value();
-    const int gs = meta.count("quantization.group_size") ? std::atoi(meta["quantization.group_size"].c_str()) : 64;
-    const int bits = meta.count("quantization.bits") ? std::atoi(meta["quantization.bits"].c_str()) : 4;
-    if (gs <= 0 || bits <= 0) return Error{MQ4_ERR_INVALID_ARG, path + ": bad quantization metadata"};
+    if (auto fr = q4_cache_format(meta, path); !fr) return fr.error();
+    const int gs = 64, bits = 4;
     std::map<std::string, QuantizedTensor> out;
     const std::string suf = ".weight";
     for (auto& [key, w] : t) {

@@ -794,9 +794,20 @@ static bool mlp_paired_ok(int64_t M, int64_t K, int64_t N, const QMat& g, const 
 
 }  // namespace mq4
 
+// Enough for every call of at most M rows: the layout's size grows with the
+// row count inside each of its three regimes (up to kMfmaMinM - 1 rows: h
+// only; to kGemmMinM - 1: h and two fp32 K parts; from kGemmMinM: h and the
+// paired operands), but the third regime needs less per row than the second,
+// so the size is the largest over the regimes' top row counts up to M.
 extern "C" size_t mq4_mlp_workspace_size(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0) return 0;
-    return mlp_ws_layout(nullptr, M, K, N).bytes;
+    size_t need = mlp_ws_layout(nullptr, M, K, N).bytes;
+    for (int64_t top : {(int64_t)kMfmaMinM - 1, (int64_t)kGemmMinM - 1}) {
+        const int64_t m = top < M ? top : M;
+        const size_t b = mlp_ws_layout(nullptr, m, K, N).bytes;
+        need = b > need ? b : need;
+    }
+    return need;
 }
 
 extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const uint16_t* norm_weight, float eps,

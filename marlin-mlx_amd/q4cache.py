@@ -79,8 +79,26 @@ def read_safetensors(path: str):
     return header, data
 
 
-def save_q4_cache(path: str, tensors: dict, group_size: int = 64, bits: int = 4) -> None:
-    """Write {name: QuantizedTensor} as name.weight / .scales / .biases."""
+def source_fingerprint(w: torch.Tensor) -> str:
+    """Shape and an exact integer checksum of a bf16 weight, computed where
+    the tensor lives: sum over i of bits_i * (i mod 65521 + 1) mod 2^64,
+    with bits_i the 16-bit pattern of element i.  It tells a cache written
+    for these source weights from one written for another checkpoint."""
+    flat = w.detach().contiguous().view(-1).view(torch.int16)
+    acc = 0
+    step = 1 << 24
+    for o in range(0, flat.numel(), step):
+        v = flat[o:o + step].to(torch.int64) & 0xFFFF
+        k = torch.arange(o, o + v.numel(), device=v.device, dtype=torch.int64) % 65521 + 1
+        acc = (acc + int((v * k).sum().item())) & 0xFFFFFFFFFFFFFFFF
+    return "x".join(str(int(d)) for d in w.shape) + f":{acc:016x}"
+
+
+def save_q4_cache(path: str, tensors: dict, group_size: int = 64, bits: int = 4,
+                  sources: dict | None = None) -> None:
+    """Write {name: QuantizedTensor} as name.weight / .scales / .biases; with
+    sources ({name: fingerprint string}) each matrix's source fingerprint is
+    recorded in the metadata as "source.<name>"."""
     entries = []
     for name, q in tensors.items():
         if not q.quantized or q.group_size != group_size or q.bits != bits:
@@ -88,8 +106,10 @@ def save_q4_cache(path: str, tensors: dict, group_size: int = 64, bits: int = 4)
         entries.append((name + ".weight", "U32", list(q.weight.shape), _tensor_bytes(q.weight)))
         entries.append((name + ".scales", "BF16", list(q.scales.shape), _tensor_bytes(q.scales)))
         entries.append((name + ".biases", "BF16", list(q.biases.shape), _tensor_bytes(q.biases)))
-    write_safetensors(path, entries, {"format": "mlx", "quantization.group_size": str(group_size),
-                                      "quantization.bits": str(bits)})
+    meta = {"format": "mlx", "quantization.group_size": str(group_size), "quantization.bits": str(bits)}
+    for name, fp in (sources or {}).items():
+        meta["source." + name] = fp
+    write_safetensors(path, entries, meta)
 
 
 def load_q4_cache(path: str, device="cuda", group_size: int | None = None, bits: int | None = None) -> dict:
@@ -101,6 +121,11 @@ def load_q4_cache(path: str, device="cuda", group_size: int | None = None, bits:
     meta = header.get("__metadata__", {}) or {}
     gs = group_size if group_size is not None else int(meta.get("quantization.group_size", 64))
     bt = bits if bits is not None else int(meta.get("quantization.bits", 4))
+    if gs != 64 or bt != 4:
+        # MLX also writes other group sizes and bit widths; this library's
+        # kernels read only the group-64, 4-bit layout
+        raise NotImplementedError(f"load_q4_cache: {path} holds group_size={gs}, bits={bt}; "
+                                  f"only group_size=64, bits=4 is implemented")
     names = sorted(k[:-len(".weight")] for k in header if k.endswith(".weight")
                    and k[:-len(".weight")] + ".scales" in header)
 
@@ -129,14 +154,22 @@ def load_q4_cache(path: str, device="cuda", group_size: int | None = None, bits:
 
 def quantize_or_load(path: str, weights: dict, device="cuda") -> dict:
     """The load-time step of the reference (quantize each bf16 weight) with a
-    cache: if `path` exists and holds every name, load it; otherwise quantize
-    the given bf16 [N, K] tensors (one batched quantize) and write the cache."""
+    cache: if `path` exists, holds every name with the weight's shape and was
+    written from these very weights (the source fingerprints recorded at
+    save time match), load it; otherwise quantize the given bf16 [N, K]
+    tensors (one batched quantize) and write the cache.  A cache left by
+    another checkpoint or model is therefore never used silently."""
     from . import quantize_weights
-    if os.path.exists(path):
-        cached = load_q4_cache(path, device)
-        if all(n in cached for n in weights):
-            return {n: cached[n] for n in weights}
     names = list(weights)
+    fps = {n: source_fingerprint(weights[n]) for n in names}
+    if os.path.exists(path):
+        header, _ = read_safetensors(path)
+        meta = header.get("__metadata__", {}) or {}
+        if all(meta.get("source." + n) == fps[n] for n in names):
+            cached = load_q4_cache(path, device)
+            if all(n in cached and (cached[n].out_features, cached[n].in_features) == tuple(weights[n].shape)
+                   for n in names):
+                return {n: cached[n] for n in names}
     out = dict(zip(names, quantize_weights([weights[n] for n in names])))
-    save_q4_cache(path, out)
+    save_q4_cache(path, out, sources=fps)
     return out

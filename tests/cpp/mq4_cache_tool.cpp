@@ -2,6 +2,8 @@
 //   mq4_cache_tool write <path>   writes a fixed set of tensors with the C++ writer
 //   mq4_cache_tool dump <path>    reads a file with the C++ reader and prints, per
 //                                 tensor (sorted by name): name dtype shape fnv1a64(bytes)
+//   mq4_cache_tool check <path>   reads a file and applies load_q4_cache's format
+//                                 check (group 64, 4 bits); exit 0 if accepted
 // tests/test_q4cache.py compares both directions with the Python module and
 // with the safetensors library.
 #include <cstdio>
@@ -20,7 +22,7 @@ static uint64_t fnv1a(const std::vector<uint8_t>& d) {
 
 int main(int argc, char** argv) {
     if (argc != 3) {
-        std::fprintf(stderr, "usage: %s write|dump <path>\n", argv[0]);
+        std::fprintf(stderr, "usage: %s write|dump|check <path>\n", argv[0]);
         return 2;
     }
     const std::string mode = argv[1], path = argv[2];
@@ -41,6 +43,20 @@ int main(int argc, char** argv) {
         if (!r) {
             std::fprintf(stderr, "%s\n", r.error().message.c_str());
             return 1;
+        }
+        return 0;
+    }
+    if (mode == "check") {
+        std::map<std::string, std::string> meta;
+        auto r = mq4::read_safetensors(path, &meta);
+        if (!r) {
+            std::fprintf(stderr, "%s\n", r.error().message.c_str());
+            return 1;
+        }
+        auto f = mq4::q4_cache_format(meta, path);
+        if (!f) {
+            std::fprintf(stderr, "error %d: %s\n", f.error().code, f.error().message.c_str());
+            return 3;
         }
         return 0;
     }

@@ -109,6 +109,58 @@ int main(int argc, char** argv) {
                     head(hidden.as<uint16_t>(), 0, final_norm.as<uint16_t>(), 1e-6f, lmq.value(), idx.as<uint32_t>(),
                          nullptr, st).ok();
     std::printf("empty_ok %d\n", empty_ok ? 1 : 0);
+
+    // MlpResidual sized for 40 rows serves every row count up to 40 (24 and
+    // 32 rows need the two fp32 K parts of the MFMA path, more per row than
+    // the paired GEMM operands of 33-40 rows); below 33 rows it gives the
+    // separate entries' bits
+    bool rows_ok = true;
+    {
+        const int64_t R = 40;
+        mq4::DeviceBuffer xa(2 * R * H), xb(2 * R * H), hb(2 * R * I);
+        mq4::MlpResidual mlp40(R, H, I);
+        for (int64_t M : {24, 32, 40}) {
+            if (fill(xa.as<uint16_t>(), M * H, 3100, 0.0, 1.0, st)) return 3;
+            if (fill(xb.as<uint16_t>(), M * H, 3100, 0.0, 1.0, st)) return 3;
+            auto r = mlp40(xa.as<uint16_t>(), M, norms[0].as<uint16_t>(), 1e-6f, layers[0], st);
+            if (!r) {
+                std::fprintf(stderr, "MlpResidual(40 rows) at M=%lld: %s\n", (long long)M, r.error().message.c_str());
+                rows_ok = false;
+                continue;
+            }
+            CHECK(mq4::mlp_forward_residual(xb.as<uint16_t>(), M, norms[0].as<uint16_t>(), 1e-6f, layers[0],
+                                            hb.as<uint16_t>(), st));
+            if (hipStreamSynchronize(st) != hipSuccess) return 4;
+            if (M < 33) {
+                std::vector<uint16_t> a(M * H), b(M * H);
+                if (hipMemcpy(a.data(), xa.get(), 2 * M * H, hipMemcpyDeviceToHost) != hipSuccess ||
+                    hipMemcpy(b.data(), xb.get(), 2 * M * H, hipMemcpyDeviceToHost) != hipSuccess)
+                    return 4;
+                rows_ok = rows_ok && a == b;
+            }
+        }
+    }
+    std::printf("mlp_residual_rows_ok %d\n", rows_ok ? 1 : 0);
+
+    // another format (group 128, or 2 bits) is refused before any launch
+    bool rejected = true;
+    {
+        mq4::MLPWeights odd;
+        odd.gate_proj.quantized = odd.up_proj.quantized = odd.down_proj.quantized = true;
+        odd.gate_proj.group_size = 128;
+        auto r = mlp(hidden2.as<uint16_t>(), 1, norms[0].as<uint16_t>(), 1e-6f, odd, st);
+        rejected = rejected && !r && r.error().code == MQ4_ERR_UNSUPPORTED;
+        auto r2 = mq4::mlp_forward_residual(hidden.as<uint16_t>(), 1, norms[0].as<uint16_t>(), 1e-6f, odd,
+                                            h.as<uint16_t>(), st);
+        rejected = rejected && !r2 && r2.error().code == MQ4_ERR_UNSUPPORTED;
+        mq4::QuantizedTensor two_bit;
+        two_bit.quantized = true;
+        two_bit.bits = 2;
+        auto r3 = head(hidden.as<uint16_t>(), 1, final_norm.as<uint16_t>(), 1e-6f, two_bit, idx.as<uint32_t>(),
+                       nullptr, st);
+        rejected = rejected && !r3 && r3.error().code == MQ4_ERR_UNSUPPORTED;
+    }
+    std::printf("format_rejected %d\n", rejected ? 1 : 0);
     (void)hipStreamDestroy(st);
     return 0;
 }

@@ -229,7 +229,17 @@ def test_mlp_residual_workspace_and_validation(mq4):
     assert L.mq4_mlp_workspace_size(32, 2048, 6144) == up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
     M, K, N = 2048, 2048, 6144
     assert L.mq4_mlp_workspace_size(M, K, N) == up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) + up(M * N // 64 * 4)
-    need = L.mq4_mlp_workspace_size(40, 2048, 6144)
+    # the size for M rows covers every call of at most M rows (the paired
+    # GEMM regime from 33 rows needs less per row than the two fp32 K parts of
+    # 5-32 rows, so the size is the largest over the regimes up to M)
+    for K, N in ((2048, 6144), (512, 1024), (6144, 2048)):
+        sizes = [L.mq4_mlp_workspace_size(m, K, N) for m in range(1, 80)]
+        assert all(b >= a for a, b in zip(sizes, sizes[1:])), (K, N)
+    assert L.mq4_mlp_workspace_size(40, 2048, 6144) >= up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
+    # the call itself needs only its own row count's layout (40 rows: the
+    # paired GEMM operands), less than the size that covers every M <= 40
+    need = up(40 * 6144 * 2) + up(40 * 2048 * 2) + up(40 * 2048 // 64 * 4) + up(40 * 6144 // 64 * 4)
+    assert need < L.mq4_mlp_workspace_size(40, 2048, 6144)
     w = [fake(A16)] * 9
     call = lambda ws, nb, **kw: L.mq4_mlp_residual(kw.get("x", fake(A16)), kw.get("M", 40), kw.get("K", 2048),
                                                    fake(A16), ctypes.c_float(1e-6), *w, kw.get("N", 6144), ws, nb,

@@ -49,3 +49,9 @@ def test_cpp_demo_matches_python_binding(mq4, O, dev):
     # mq4::MlpResidual (one mq4_mlp_residual call per layer) gave the same hidden state
     assert lines[3] == "mlp_residual_same 1"
     assert lines[4] == "empty_ok 1"
+    # mq4::MlpResidual sized for 40 rows runs 24, 32 and 40 rows (a workspace
+    # size that never shrinks as the row count grows), and bit for bit the
+    # separate entries' result below 33 rows
+    assert lines[5] == "mlp_residual_rows_ok 1"
+    # tensors of another format are refused by the fused mirrors
+    assert lines[6] == "format_rejected 1"

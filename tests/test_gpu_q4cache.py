@@ -41,11 +41,29 @@ def test_quantize_or_load_uses_the_cache(mq4, dev, tmp_path, monkeypatch):
     first = mq4.quantize_or_load(path, ws, device=dev)
     assert os.path.exists(path)
     calls = []
-    monkeypatch.setattr(mq4, "quantize_weight", lambda *a, **k: calls.append(1) or (_ for _ in ()).throw(
-        AssertionError("quantize_weight called although the cache exists")))
+    monkeypatch.setattr(mq4, "quantize_weights", lambda *a, **k: calls.append(1) or (_ for _ in ()).throw(
+        AssertionError("quantize_weights called although the cache exists")))
     second = mq4.quantize_or_load(path, ws, device=dev)
     assert not calls
     assert torch.equal(first["lm_head"].weight, second["lm_head"].weight)
+
+
+def test_quantize_or_load_ignores_a_stale_cache(mq4, dev, tmp_path):
+    """A cache written from other weights under the same names (another
+    checkpoint), or with other shapes, is not used: the weights passed in are
+    quantized again and the cache is rewritten for them."""
+    path = str(tmp_path / "s.safetensors")
+    a = {"lm_head": mq4.fill_normal_bf16((4096, 2048), 2000, 0.0, 0.02, device=dev)}
+    b = {"lm_head": mq4.fill_normal_bf16((4096, 2048), 2002, 0.0, 0.02, device=dev)}
+    c = {"lm_head": mq4.fill_normal_bf16((2048, 2048), 2000, 0.0, 0.02, device=dev)}
+    qa = mq4.quantize_or_load(path, a, device=dev)["lm_head"]
+    for ws in (b, c, a):
+        got = mq4.quantize_or_load(path, ws, device=dev)["lm_head"]
+        want = mq4.quantize_weight(ws["lm_head"])
+        torch.cuda.synchronize()
+        assert torch.equal(got.weight, want.weight)
+        assert torch.equal(got.scales.view(torch.int16), want.scales.view(torch.int16))
+    assert not torch.equal(qa.weight[:2048], mq4.quantize_weight(b["lm_head"]).weight[:2048])
 
 
 def test_cpp_cache_round_trip_keeps_the_token(mq4, dev, tmp_path):

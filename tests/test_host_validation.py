@@ -96,3 +96,27 @@ def test_decode_step_checks_every_layer(mq4):
     # all shapes right: the remaining complaint is that the tensors are host memory
     with pytest.raises(ValueError, match="device"):
         mq4.DecodeStep([mq4.DecoderLayer(fn, good)], fn, lm)
+
+
+def test_fused_paths_reject_other_formats(mq4):
+    """The kernels read the group-64, 4-bit layout only.  A tensor that
+    claims another format (as a cache file MLX wrote with group 128 or 2 bits
+    would give) is refused before its buffers reach an entry point; with
+    group 128 the scales/biases of a matching shape would otherwise be read
+    as if they held K/64 groups."""
+    g = qt(mq4, 64, 2048)
+    odd = mq4.QuantizedTensor(torch.zeros((64, 2048 // 8), dtype=torch.int32),
+                              torch.zeros((64, 2048 // 128), dtype=torch.bfloat16),
+                              torch.zeros((64, 2048 // 128), dtype=torch.bfloat16), 128, 4, True)
+    two_bit = mq4.QuantizedTensor(torch.zeros((64, 2048 * 2 // 32), dtype=torch.int32),
+                                  torch.zeros((64, 32), dtype=torch.bfloat16),
+                                  torch.zeros((64, 32), dtype=torch.bfloat16), 64, 2, True)
+    for bad in (odd, two_bit):
+        with pytest.raises(NotImplementedError, match="group_size=64, bits=4"):
+            mq4.mlp_gate_up_silu(x_of(1, 2048), g, bad)
+        with pytest.raises(NotImplementedError, match="group_size=64, bits=4"):
+            mq4.lm_head_argmax(x_of(1, 2048), bad)
+        with pytest.raises(NotImplementedError, match="group_size=64, bits=4"):
+            mq4.qmatmul(x_of(1, 2048), bad)
+        with pytest.raises(NotImplementedError, match="group_size=64, bits=4"):
+            mq4.mlp_residual(x_of(1, 2048), mq4.MLPWeights(g, g, bad), torch.zeros(2048, dtype=torch.bfloat16))

@@ -127,3 +127,63 @@ def test_malformed_files_are_rejected(mq4, tmp_path):
                "a.biases": q.biases[:, :1].contiguous()}, p)
     with pytest.raises(ValueError, match="do not match"):
         mq4.load_q4_cache(p, device="cpu")
+
+
+@pytest.mark.parametrize("meta", [{"quantization.group_size": "128", "quantization.bits": "4"},
+                                  {"quantization.group_size": "64", "quantization.bits": "2"}])
+def test_other_formats_are_refused_by_both_loaders(mq4, tmp_path, meta):
+    """MLX writes other group sizes and bit widths too.  Both loaders refuse
+    them: the fused entry points take no format argument and would read a
+    group-128 file's scales as K/64 groups, past their end."""
+    from safetensors.torch import save_file
+    K = 256
+    bits = int(meta["quantization.bits"])
+    gs = int(meta["quantization.group_size"])
+    g = torch.Generator().manual_seed(9)
+    wq = torch.randint(0, 2 ** 31 - 1, (8, K * bits // 32), generator=g, dtype=torch.int64).to(torch.int32)
+    s = torch.zeros((8, K // gs), dtype=torch.bfloat16)
+    p = str(tmp_path / "other.safetensors")
+    save_file({"a.weight": wq.view(torch.uint32), "a.scales": s, "a.biases": s.clone()}, p, metadata=meta)
+    with pytest.raises(NotImplementedError, match="group_size=64, bits=4"):
+        mq4.load_q4_cache(p, device="cpu")
+    r = subprocess.run([TOOL, "check", p], capture_output=True, text=True, timeout=30)
+    assert r.returncode == 3 and "group_size=64, bits=4" in r.stderr, r.stderr
+    good = str(tmp_path / "good.safetensors")
+    mq4.save_q4_cache(good, {"a": random_q4(mq4, 4, 128, 6)})
+    assert subprocess.run([TOOL, "check", good], capture_output=True, timeout=30).returncode == 0
+
+
+def test_crafted_headers_are_rejected_by_cpp_reader(tmp_path):
+    """A shape whose element count overflows 64 bits (it would wrap around to
+    match the data offsets) and a header nested past any safetensors layout
+    (recursion depth) are refused by the C++ reader."""
+    def write(name, header: bytes, data: bytes = b"\0" * 16):
+        header += b" " * (-len(header) % 8)
+        p = str(tmp_path / name)
+        with open(p, "wb") as f:
+            f.write(struct.pack("<Q", len(header)) + header + data)
+        return p
+    # 2^32 * 2^32 * 4 wraps to 0 in 64-bit arithmetic: the same as offsets [0, 0]
+    wrap = write("wrap.safetensors", b'{"a.weight":{"dtype":"U32","shape":[4294967296,4294967296],'
+                                     b'"data_offsets":[0,0]}}')
+    r = subprocess.run([TOOL, "dump", wrap], capture_output=True, text=True, timeout=30)
+    assert r.returncode != 0 and "shape" in r.stderr
+    deep = write("deep.safetensors", b'{"__metadata__":' + b"[" * 100000 + b"]" * 100000 + b"}")
+    r = subprocess.run([TOOL, "dump", deep], capture_output=True, text=True, timeout=30)
+    assert r.returncode == 1 and "JSON" in r.stderr
+
+
+def test_source_fingerprint(mq4):
+    """The fingerprint quantize_or_load compares: equal for equal weights,
+    different when any element or the shape differs."""
+    from importlib import import_module
+    qc = import_module(mq4.__name__ + ".q4cache")
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn((64, 128), generator=g).to(torch.bfloat16)
+    a = qc.source_fingerprint(w)
+    assert a == qc.source_fingerprint(w.clone())
+    w2 = w.clone()
+    w2[63, 127] = w2[63, 127] + 1
+    assert qc.source_fingerprint(w2) != a
+    assert qc.source_fingerprint(w.reshape(128, 64)) != a
+    assert a.startswith("64x128:")
