@@ -149,6 +149,21 @@ class Env:
         del w
         return Q4(wq, s, b, N, K)
 
+    def per_launch(self, fn, n, warm=1):
+        """Statistics of fn() timed one launch at a time: a HIP event pair on the
+        launch stream around each of n calls (the events add a marker packet
+        between launches, so these are per-launch durations, not throughput)."""
+        for _ in range(warm):
+            fn()
+        self.torch.cuda.synchronize()
+        evs = [(self.ev(), self.ev()) for _ in range(n)]
+        for a, b in evs:
+            a.record()
+            fn()
+            b.record()
+        self.torch.cuda.synchronize()
+        return launch_stats([a.elapsed_time(b) * 1e3 for a, b in evs])
+
     def timed(self, fn, n, warm=1):
         """Mean microseconds of fn() launched n times back to back, HIP events on
         the launch stream around the batch."""
@@ -162,6 +177,14 @@ class Env:
         e1.record()
         self.torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / n
+
+
+def launch_stats(us):
+    """median / p10 / p90 / min / max / mean of per-launch microseconds."""
+    v = sorted(us)
+    q = lambda f: v[min(len(v) - 1, max(0, int(round(f * (len(v) - 1)))))]
+    return {"n": len(v), "median": round(q(0.5), 2), "p10": round(q(0.1), 2), "p90": round(q(0.9), 2),
+            "min": round(v[0], 2), "max": round(v[-1], 2), "mean": round(sum(v) / len(v), 2)}
 
 
 def hbm_roofline(nbytes, us):
@@ -341,6 +364,9 @@ def main():
         raise RuntimeError("one-launch decode step: token changed across launches")
     gbps = STEP_BYTES / (ms_step * 1e-3) / 1e9
     log(f"[bench] step {ms_step * 1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
+    # the same launches one at a time, each between its own pair of events
+    step_stats = E.per_launch(lambda: L.mq4_decode_step(*dargs(st)), args.steps, warm=2)
+    log(f"[bench] per-launch step durations: {step_stats}")
     # the same kernel replayed from a HIP graph (for callers that capture)
     pgraph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
@@ -356,7 +382,7 @@ def main():
                               "us_per_step": round(ms_step * 1e3, 2),
                               "bytes_per_launch": KERNEL_BYTES["decode_step"],
                               "GBps": round(KERNEL_BYTES["decode_step"] / (ms_step * 1e-3) / 1e9, 1),
-                              "graph_replay_us": round(us_graph, 2)}
+                              "graph_replay_us": round(us_graph, 2), "per_launch_us": step_stats}
     roofline = {"kernel": "decode_step", **hbm_roofline(KERNEL_BYTES["decode_step"], ms_step * 1e3),
                 "traffic": measured_traffic()}
 
@@ -365,7 +391,9 @@ def main():
     if not args.no_configs:
         for name, fn in (("config1_gemv_gate", lambda: bench_gemv_gate(E, layers, x0)),
                          ("config2_mlp_chain", lambda: bench_mlp_chain(E, dec_layers, lm, norm_w, x0)),
-                         ("config3_lm_head_argmax", lambda: bench_lm_head(E, lm, norm_w, x0)),
+                         ("config3_lm_head_argmax", lambda: bench_lm_head(E, lm, norm_w, x0, dstep)),
+                         ("integration_per_layer", lambda: bench_per_layer(E, dstep, layers, lm, norm_w, layer_norms,
+                                                                           x0, tok_p)),
                          ("config4_prefill", lambda: bench_prefill(E, layers, args, layer_norms)),
                          ("config5a_batched", lambda: bench_batched(E, layers, lm, norm_w, layer_norms)),
                          ("config5b_pack", lambda: bench_pack(E, layers, lm)),
@@ -405,6 +433,7 @@ def main():
             "M": 1,
             "weight_bytes_per_step": STEP_BYTES,
             "us_per_step": round(ms_step * 1e3, 2),
+            "us_per_launch_median_p10_p90": [step_stats["median"], step_stats["p10"], step_stats["p90"]],
             "pct_of_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
             "parallelism": "single GPU",
         },
@@ -441,12 +470,37 @@ def bench_gemv_gate(E, layers, x0):
                    warm=1) / len(mats)
     m0 = mats[0]
     warm = E.timed(lambda: L.mq4_qmm(xp, 1, HID, *m0.ptrs(), INTER, 1, 64, 4, yp, st), 200, warm=20)
+
+    # the same launches replayed from HIP graphs: no host launch gaps, only the
+    # device's own dispatch gap between consecutive kernels
+    def graph_per_launch(fns, reps):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for f in fns:
+                f(P(side.cuda_stream))
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g_ = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_):
+            for f in fns:
+                f(E.st())
+        us_ = E.timed(g_.replay, reps, warm=2) / len(fns)
+        del g_
+        return us_
+
+    qmm = lambda m: (lambda s_: L.mq4_qmm(xp, 1, HID, *m.ptrs(), INTER, 1, 64, 4, yp, s_))
+    cold_g = graph_per_launch([qmm(m) for m in mats], 10)
+    warm_g = graph_per_launch([qmm(m0)] * len(mats), 10)
     del extra
     return {"shape": "M=1, N=6144, K=2048 (gate_proj)", "bytes_per_launch": nbytes,
-            "cold_us": round(cold, 3), "warm_us": round(warm, 3),
-            "roofline_cold": hbm_roofline(nbytes, cold), "roofline_warm": hbm_roofline(nbytes, warm),
-            "note": "back-to-back launches between HIP events on the launch stream; cold rotates over "
-                    "80 distinct matrices (566 MB > 2 x 256 MB last-level cache); warm repeats one "
+            "cold_us": round(cold_g, 3), "warm_us": round(warm_g, 3),
+            "roofline_cold": hbm_roofline(nbytes, cold_g), "roofline_warm": hbm_roofline(nbytes, warm_g),
+            "cold_back_to_back_us": round(cold, 3), "warm_back_to_back_us": round(warm, 3),
+            "note": "cold_us / warm_us: HIP graph of 80 launches replayed, time per launch (the device's "
+                    "dispatch gap between kernels included, no host launch gaps; the rooflines use it); "
+                    "back_to_back: the same launches issued from the host one after another; cold rotates "
+                    "over 80 distinct matrices (566 MB > 2 x 256 MB last-level cache), warm repeats one "
                     "(served from that cache, so its rate exceeds HBM)"}
 
 
@@ -469,21 +523,119 @@ def bench_mlp_chain(E, dec_layers, lm, norm_w, x0):
                     "are the only extra work)"}
 
 
-def bench_lm_head(E, lm, norm_w, x0):
-    """Config 3: final RMSNorm + lm_head 248320x2048 + greedy argmax, M=1."""
+def bench_per_layer(E, dstep, layers, lm, norm_w, layer_norms, x0, tok):
+    """The headline step as the reference's layer loop can call it (its
+    attention / SSM half runs between the MLP halves, src/model/marlin.cpp:
+    110-143): 24 separate calls of one MLP half each, then the final norm +
+    lm_head + argmax, replayed from a HIP graph (as a serving loop would
+    capture it).  Two call structures: the one-launch MLP half
+    (mq4_decode_step with one layer and vocab 0; one-launch lm_head:
+    mq4_decode_step with no layers) and mq4_mlp_residual at M = 1 (two
+    kernels per layer) + mq4_rmsnorm_lm_head_argmax.  Both must give the
+    headline token."""
+    torch, L, P = E.torch, E.L, E.P
+    a = torch.empty((HID,), dtype=torch.bfloat16, device=E.dev)
+    b = torch.empty_like(a)
+    idx = torch.zeros((1,), dtype=torch.int32, device=E.dev)
+    sz = ctypes.sizeof(type(dstep._arr[0]))
+    base = ctypes.addressof(dstep._arr)
+    mwsb = L.mq4_mlp_workspace_size(1, HID, INTER)
+    mws = torch.empty(mwsb, dtype=torch.uint8, device=E.dev)
+    lwsb = L.mq4_lm_head_argmax_workspace_size(1, VOCAB)
+    lws = torch.zeros(lwsb, dtype=torch.uint8, device=E.dev)
+
+    def one_launch(st):
+        src = P(x0.data_ptr())
+        for l in range(LAYERS):
+            dst = a if l % 2 == 0 else b
+            E.mq4._check(L.mq4_decode_step(src, HID, INTER, 1, P(base + l * sz), None, EPS, None, None, None, 0,
+                                           None, P(dst.data_ptr()), P(dstep.workspace.data_ptr()), dstep.ws_bytes,
+                                           st))
+            src = P(dst.data_ptr())
+        E.mq4._check(L.mq4_decode_step(src, HID, INTER, 0, None, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB,
+                                       P(idx.data_ptr()), None, P(dstep.workspace.data_ptr()), dstep.ws_bytes, st))
+
+    def two_kernel(st):
+        src = P(x0.data_ptr())
+        for l, (g, u, d) in enumerate(layers):
+            dst = a if l % 2 == 0 else b
+            E.mq4._check(L.mq4_mlp_residual(src, 1, HID, P(layer_norms[l].data_ptr()), EPS, *g.ptrs(), *u.ptrs(),
+                                            *d.ptrs(), INTER, P(mws.data_ptr()), mwsb, P(dst.data_ptr()), st))
+            src = P(dst.data_ptr())
+        E.mq4._check(L.mq4_rmsnorm_lm_head_argmax(src, 1, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(), VOCAB,
+                                                  P(idx.data_ptr()), None, P(lws.data_ptr()), lwsb, st))
+
+    def graph_us(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn(P(side.cuda_stream))
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        if int(idx.item()) != tok:
+            raise RuntimeError(f"integration_per_layer: token {int(idx.item())} differs from the step's {tok}")
+        g_ = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_):
+            fn(E.st())
+        us_ = E.timed(g_.replay, 20, warm=3)
+        idx.fill_(-1)
+        g_.replay()
+        torch.cuda.synchronize()
+        if int(idx.item()) != tok:
+            raise RuntimeError("integration_per_layer: graph replay token differs")
+        del g_
+        return us_
+
+    us_one = graph_us(one_launch)
+    us_two = graph_us(two_kernel)
+    # one MLP half alone (the per-layer call), per launch
+    st = E.st()
+    half = E.per_launch(lambda: L.mq4_decode_step(P(x0.data_ptr()), HID, INTER, 1, P(base), None, EPS, None, None,
+                                                  None, 0, None, P(a.data_ptr()), P(dstep.workspace.data_ptr()),
+                                                  dstep.ws_bytes, st), 100, warm=5)
+    return {"workload": "24 x one-call MLP half (M=1) + final norm + lm_head 248320 + argmax, each call "
+                        "separate (the reference loop runs attention / SSM between them), HIP graph replay",
+            "one_launch_mlp_half_us_per_step": round(us_one, 1),
+            "one_launch_roofline": hbm_roofline(STEP_BYTES, us_one),
+            "mlp_residual_two_kernels_us_per_step": round(us_two, 1),
+            "mlp_residual_roofline": hbm_roofline(STEP_BYTES, us_two),
+            "one_launch_mlp_half_per_launch_us": half, "token": tok,
+            "note": "one-launch MLP half = mq4_decode_step(n_layers=1, vocab=0), the whole MLP half of a "
+                    "layer in one persistent launch; the lm_head there is mq4_decode_step(n_layers=0)"}
+
+
+def bench_lm_head(E, lm, norm_w, x0, dstep):
+    """Config 3: final RMSNorm + lm_head 248320x2048 + greedy argmax, M=1, two
+    ways: mq4_rmsnorm_lm_head_argmax (GEMV with per-block argmax keys, then a
+    finalize launch; its workspace needs no initialisation) and the one-launch
+    decode step with no layers (its lm_head phase, keys reduced inside the
+    launch through tagged words; workspace zero-filled once).  Both must give
+    the same token; `us` is the faster."""
     torch, L, P = E.torch, E.L, E.P
     idx = torch.zeros((1,), dtype=torch.int32, device=E.dev)
+    idx1 = torch.zeros((1,), dtype=torch.int32, device=E.dev)
     wsb = L.mq4_lm_head_argmax_workspace_size(1, VOCAB)
     ws = torch.zeros(wsb, dtype=torch.uint8, device=E.dev)
     st = E.st()
     f = lambda: L.mq4_rmsnorm_lm_head_argmax(P(x0.data_ptr()), 1, HID, P(norm_w.data_ptr()), EPS, *lm.ptrs(),
                                              VOCAB, P(idx.data_ptr()), None, P(ws.data_ptr()), wsb, st)
-    us = E.timed(f, 50, warm=5)
+    g = lambda: L.mq4_decode_step(P(x0.data_ptr()), HID, INTER, 0, None, P(norm_w.data_ptr()), EPS, *lm.ptrs(),
+                                  VOCAB, P(idx1.data_ptr()), None, P(dstep.workspace.data_ptr()), dstep.ws_bytes, st)
+    us_two = E.timed(f, 50, warm=5)
+    us_one = E.timed(g, 50, warm=5)
+    if int(idx.item()) != int(idx1.item()):
+        raise RuntimeError(f"config3: one-launch token {int(idx1.item())} != two-launch token {int(idx.item())}")
+    one_stats = E.per_launch(g, 50, warm=2)
     nbytes = KERNEL_BYTES["norm_lm_head_argmax"]
+    us = min(us_one, us_two)
     return {"shape": "M=1, N=248320, K=2048 (+ (1+w) RMSNorm, greedy argmax)", "bytes_per_call": nbytes,
             "us": round(us, 2), "roofline": hbm_roofline(nbytes, us), "token": int(idx.item()),
-            "note": "two launches per call (GEMV with per-block argmax keys, 4 us finalize); the "
-                    "286 MB weight stream exceeds the last-level cache"}
+            "one_launch_us": round(us_one, 2), "one_launch_per_launch_us": one_stats,
+            "two_launch_us": round(us_two, 2),
+            "note": "us is the faster of: one launch (mq4_decode_step with no layers: norm, lm_head GEMV and "
+                    "the argmax reduced in the launch) and mq4_rmsnorm_lm_head_argmax (GEMV with per-block "
+                    "argmax keys + a 4 us finalize launch); the 286 MB weight stream exceeds the last-level "
+                    "cache"}
 
 
 def bench_prefill(E, layers, args, layer_norms):

@@ -733,6 +733,31 @@ class DecodeStep:
                                      _stream(x.device)))
         return idx
 
+    def mlp_layer(self, i: int, x: torch.Tensor, x_out: torch.Tensor) -> torch.Tensor:
+        """x_out = x + mlp_forward(rms_norm(x, layers[i].post_attn_norm)) for one
+        token in one launch: the MLP half that the reference's layer loop runs
+        between its attention / SSM halves (src/model/marlin.cpp:141-142), so a
+        caller that interleaves other work per layer keeps the one-launch
+        exchange structure (mq4_decode_step with one layer and vocab 0, on
+        this object's workspace).  Bit-identical to the i-th layer of the
+        whole step and to the separate entry points.  x_out may not alias x."""
+        fn = "DecodeStep.mlp_layer"
+        if not 0 <= i < len(self.layers):
+            raise IndexError(f"{fn}: layer {i} of {len(self.layers)}")
+        x = _need(x, torch.bfloat16, "x")
+        if x.numel() != self.hidden:
+            raise ValueError(f"{fn}: x must hold {self.hidden} values (one token)")
+        if (not isinstance(x_out, torch.Tensor) or x_out.dtype != torch.bfloat16 or x_out.numel() != self.hidden
+                or not x_out.is_contiguous()):
+            raise ValueError(f"{fn}: x_out must be a contiguous bf16 tensor of hidden values")
+        if x_out.data_ptr() == x.data_ptr():
+            raise ValueError(f"{fn}: x_out must not alias x (workgroups read x while others write x_out)")
+        layer_ptr = ctypes.c_void_p(ctypes.addressof(self._arr) + i * ctypes.sizeof(_MlpLayerC))
+        _check(lib().mq4_decode_step(_ptr(x), self.hidden, self.intermediate, 1, layer_ptr, None, self.eps,
+                                     None, None, None, 0, None, _ptr(x_out), _ptr(self.workspace), self.ws_bytes,
+                                     _stream(x.device)))
+        return x_out
+
 
 # on-disk Q4 weight cache (safetensors, MLX naming): see q4cache.py
 from .q4cache import load_q4_cache, quantize_or_load, save_q4_cache  # noqa: E402

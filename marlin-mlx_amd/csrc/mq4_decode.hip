@@ -8,7 +8,9 @@
 // MLP half of each layer (rms_norm :141, mlp_forward :31-35, residual :142),
 // then the final norm (:145), lm_head (:161-169) and greedy sample_token
 // (src/sampling/sampler.cpp:14-16), with the same arithmetic as the separate
-// kernels of mq4_gemv.hip.
+// kernels of mq4_gemv.hip.  With vocab = 0 the launch ends after the layers
+// (one MLP half per call, as the reference's layer loop needs between its
+// attention / SSM halves).
 //
 // Why one launch: the step is 2 * layers + 1 dependent phases.  Separate
 // kernels drain the memory pipeline at every boundary (every phase pays the
@@ -34,6 +36,8 @@
 // workgroup barriers (on gfx950 a barrier waits for LDS only, not for
 // outstanding global loads).  Every wait is bounded: on a timeout a sticky
 // error word is set, every workgroup leaves, and the token reads 0xFFFFFFFF.
+#include <mutex>
+
 #include "mq4_device.h"
 #include "mq4_host.h"
 
@@ -67,11 +71,11 @@ struct Layer {
 struct Params {
     const uint16_t* x_in;      // [H] bf16
     uint16_t* x_out;           // [H] bf16 hidden state after the last layer (may be null)
-    uint32_t* idx;             // [1] token
+    uint32_t* idx;             // [1] token (unused when vocab == 0)
     const uint16_t* final_norm;
     float eps;
     QMat lm;
-    int vocab;
+    int vocab;                 // 0: layers only (no final norm, lm_head or token)
     int n_layers;
     uint64_t* xbuf;            // [kCopies][H/2] tagged words
     uint64_t* hbuf;            // [kCopies][I/2] tagged words
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     __syncthreads();
     const uint32_t base = sm.epoch * 128u + 1u;  // phase tags base + [0, 2*layers+1]: never 0, disjoint per call
     if (sm.abort) {
-        if (wg == 0 && threadIdx.x == 0) p.idx[0] = 0xffffffffu;
+        if (wg == 0 && threadIdx.x == 0 && p.vocab > 0) p.idx[0] = 0xffffffffu;
         return;
     }
 
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         // chunk lane%4), loaded one layer ahead of its use
         const int nchunk = (io * (SA / kNIO) + (lane >> 2)) * 4 + (lane & 3);
         auto norm_of = [&](int l) { return l < L ? p.layers[l].norm : p.final_norm; };
-        uint4 nw = reinterpret_cast<const uint4*>(norm_of(0))[nchunk];
+        uint4 nw = reinterpret_cast<const uint4*>(norm_of(0))[nchunk];    // L > 0 or vocab > 0
         // the copy of the exchange buffers this workgroup reads
         const uint64_t* xcopy = p.xbuf + (size_t)(wg % kCopies) * (H / 2);
         const uint64_t* hcopy = p.hbuf + (size_t)(wg % kCopies) * (I / 2);
@@ -322,6 +326,9 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         }
         lds_barrier();                                         // B0: gate/up weights of layer 0 staged
         for (int l = 0; l <= L; ++l) {
+            // layers only: the last layer's x words (and x_out) are written;
+            // nothing reads them in this launch
+            if (l == L && p.vocab == 0) break;
             // ---- x of layer l (the input at l == 0) -> xraw ----
             if (l == 0) {
 #pragma unroll
@@ -340,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
             stage_norm_x(sm, nw, p.eps, io, lane);
             lds_barrier();                                     // B2: xp/xs ready
             if (l == L) break;
-            nw = reinterpret_cast<const uint4*>(norm_of(l + 1))[nchunk];
+            if (l + 1 < L || p.vocab > 0) nw = reinterpret_cast<const uint4*>(norm_of(l + 1))[nchunk];
             if (l + 1 < L) {
                 dmaA(2 * io, l + 1, 1);
                 dmaA(2 * io + 1, l + 1, 1);
@@ -368,6 +375,12 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
             stage_h(sm, io, lane);
             lds_barrier();                                     // B4: hp/hs ready
             if (sm.abort) break;
+            if (p.vocab == 0 && l == L - 1 && wg == 0 && io == 0 && lane == 0) {
+                // layers only (no final gather): the last layer's h words came
+                // from every workgroup, so every one has read the epoch; the
+                // next call may take the next one
+                __hip_atomic_store(p.ctrl, sm.epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             if (l + 1 < L) {
                 dmaB(2 * io, l + 1);
                 dmaB(2 * io + 1, l + 1);
@@ -388,6 +401,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         wait_vmcnt<0>();                                       // no DMA may outlive the workgroup
         // ---- argmax: this workgroup's best key, then workgroup 0 reduces ----
         __syncthreads();                                       // B6: sm.best filled
+        if (p.vocab == 0) return;
         const uint32_t tag16 = (sm.epoch % 65535u) + 1u;
         if (!sm.abort && io == 0) {
             uint64_t b = lane < kNCW ? sm.best[lane] : 0ull;
@@ -588,14 +602,14 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     // (first two batches issued here, once the layer weights are dead, so they
     // are in flight during the exchange of the last hidden state)
     uint64_t best = 0;
-    if (!aborted) {
+    if (!aborted && p.vocab > 0) {
 #pragma unroll
         for (int b = 0; b < LM_NBUF; ++b)
             if (b < lm_rounds) loadLM(lb[b], b);
         lds_barrier();                                         // B1 (x of the last layer)
         if (sm.abort) aborted = true;
     }
-    if (!aborted) {
+    if (!aborted && p.vocab > 0) {
         lds_barrier();                                         // B2 (final-normalized x)
         uint32_t xp[16];
 #pragma unroll
@@ -633,7 +647,11 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
 
 }  // namespace dec
 
-static int g_dec_ok = -1;
+// Co-residency of the 256 workgroups, checked once per device.
+constexpr int kMaxDecDevices = 64;
+static int g_dec_ok[kMaxDecDevices];
+static bool g_dec_checked[kMaxDecDevices];
+static std::mutex g_dec_mu;
 
 // Poll iterations before a wait gives up (each iteration is one round trip
 // to L2 plus a short sleep, about 1 us): about a second.
@@ -664,11 +682,16 @@ extern "C" int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t int
                     dec::I, (long long)hidden, (long long)intermediate);
     if (n_layers < 0 || n_layers > dec::kMaxLayers)
         return fail(MQ4_ERR_UNSUPPORTED, "%s: n_layers must be in [0, %d]", what, dec::kMaxLayers);
-    if (vocab <= 0 || vocab > (1LL << 30))
-        return fail(MQ4_ERR_INVALID_ARG, "%s: vocab must be in [1, 2^30]", what);
-    if (!x_in || !final_norm || !lm_wq || !lm_scales || !lm_biases || !idx || (n_layers > 0 && !layers))
+    if (vocab < 0 || vocab > (1LL << 30))
+        return fail(MQ4_ERR_INVALID_ARG, "%s: vocab must be in [0, 2^30]", what);
+    if (vocab == 0 && n_layers == 0)
+        return fail(MQ4_ERR_INVALID_ARG, "%s: nothing to do (no layers and vocab 0)", what);
+    if (!x_in || (n_layers > 0 && !layers))
         return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer", what);
-    if (!aligned(x_in, 16) || !aligned(final_norm, 16) || !aligned(lm_wq, 16) || (x_out && !aligned(x_out, 4)))
+    if (vocab > 0 && (!final_norm || !lm_wq || !lm_scales || !lm_biases || !idx))
+        return fail(MQ4_ERR_INVALID_ARG, "%s: null pointer (final norm, lm_head or idx)", what);
+    if (!aligned(x_in, 16) || (x_out && !aligned(x_out, 4)) ||
+        (vocab > 0 && (!aligned(final_norm, 16) || !aligned(lm_wq, 16))))
         return fail(MQ4_ERR_ALIGNMENT, "%s: x_in, norms and packed weights must be 16-byte aligned", what);
     const size_t need = mq4_decode_workspace_size(hidden, intermediate, vocab);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
@@ -693,18 +716,24 @@ extern "C" int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t int
                        {s.up_wq, s.up_scales, s.up_biases},
                        {s.down_wq, s.down_scales, s.down_biases}};
     }
-    if (g_dec_ok < 0) {
-        int dev = 0, cus = 0, occ = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, dec::decode_step_kernel, dec::kThreads, 0) !=
-                hipSuccess)
-            return fail(MQ4_ERR_HIP, "%s: device query failed", what);
-        g_dec_ok = (cus >= dec::kNWG && occ >= 1) ? 1 : 0;
+    {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDecDevices)
+            return fail(MQ4_ERR_HIP, "%s: hipGetDevice failed", what);
+        std::lock_guard<std::mutex> lk(g_dec_mu);
+        if (!g_dec_checked[dev]) {
+            int cus = 0, occ = 0;
+            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, dec::decode_step_kernel, dec::kThreads, 0) !=
+                    hipSuccess)
+                return fail(MQ4_ERR_HIP, "%s: device query failed", what);
+            g_dec_ok[dev] = (cus >= dec::kNWG && occ >= 1) ? 1 : 0;
+            g_dec_checked[dev] = true;
+        }
+        if (g_dec_ok[dev] == 0)
+            return fail(MQ4_ERR_UNSUPPORTED, "%s: needs %d co-resident workgroups of %d threads", what, dec::kNWG,
+                        dec::kThreads);
     }
-    if (g_dec_ok == 0)
-        return fail(MQ4_ERR_UNSUPPORTED, "%s: needs %d co-resident workgroups of %d threads", what, dec::kNWG,
-                    dec::kThreads);
     p.x_in = x_in;
     p.x_out = x_out;
     p.idx = idx;

@@ -19,6 +19,9 @@
  *   mq4o_qmm_f64          mx::quantized_matmul(x, w, s, b, transpose=true, 64, 4)
  *                         (src/model/marlin.cpp:18-25, 161-169) evaluated exactly
  *                         in fp64 over the dequantized weights (the fp64 oracle).
+ *   mq4o_qmm_f64_x32      the same fp64 product on float32 x (the C++ promotion
+ *                         reading, in which float32 activations reach qmatmul and
+ *                         MLX promotes the bf16 scales and biases to float32).
  *   mq4o_qmm_f32          same product, fp32 accumulation, OpenMP over rows
  *                         (CPU baseline "all cores" mode).
  *   mq4o_qmm_mlx_bf16     the literal scalar loop of MLX's CPU _qmm_t for T=bf16
@@ -78,6 +81,7 @@
 #include <math.h>
 #include <omp.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <stddef.h>
 #include <string.h>
 
@@ -259,25 +263,65 @@ void mq4o_qmm_f64(const uint16_t* x, int64_t M, int64_t K, const uint32_t* wq,
                   const uint16_t* scales, const uint16_t* biases, int64_t N,
                   double* y, uint16_t* y_bf16) {
     const int64_t G = K / MQ4O_GROUP;
-#pragma omp parallel for schedule(static)
-    for (int64_t n = 0; n < N; ++n) {
-        for (int64_t m = 0; m < M; ++m) {
-            const uint16_t* xr = x + m * K;
-            double acc = 0.0;
+#pragma omp parallel
+    {
+        /* row n dequantized once (w = s*q + b, exact in fp64), then dotted with
+         * every row of x in k order */
+        double* w = (double*)malloc((size_t)K * sizeof(double));
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < N; ++n) {
             for (int64_t g = 0; g < G; ++g) {
                 double s = bf16_to_f32(scales[n * G + g]);
                 double b = bf16_to_f32(biases[n * G + g]);
                 for (int j = 0; j < 8; ++j) {
                     uint32_t word = wq[n * (K / 8) + g * 8 + j];
-                    for (int p = 0; p < 8; ++p) {
-                        double w = s * (double)((word >> (4 * p)) & 0xfu) + b;
-                        acc += (double)bf16_to_f32(xr[g * 64 + j * 8 + p]) * w;
-                    }
+                    for (int p = 0; p < 8; ++p) w[g * 64 + j * 8 + p] = s * (double)((word >> (4 * p)) & 0xfu) + b;
                 }
             }
-            if (y) y[m * N + n] = acc;
-            if (y_bf16) y_bf16[m * N + n] = f64_to_bf16(acc);
+            for (int64_t m = 0; m < M; ++m) {
+                const uint16_t* xr = x + m * K;
+                double acc = 0.0;
+                for (int64_t k = 0; k < K; ++k) acc += (double)bf16_to_f32(xr[k]) * w[k];
+                if (y) y[m * N + n] = acc;
+                if (y_bf16) y_bf16[m * N + n] = f64_to_bf16(acc);
+            }
         }
+        free(w);
+    }
+}
+
+/* mx::quantized_matmul on float32 x (src/model/marlin.cpp:18-25 when the
+ * activation reaching qmatmul is float32, as in the C++ promotion reading of
+ * rms_norm: MLX then promotes the bf16 scales and biases to float32, exactly),
+ * evaluated in fp64 over the dequantized weights like mq4o_qmm_f64: each
+ * weight row is dequantized once and dotted with every row of x, products and
+ * sums in fp64 (y[m, n] is the true value to ~1e-16 relative).  For x whose
+ * values are bf16-representable it equals mq4o_qmm_f64 on the same values bit
+ * for bit (same terms, same order). */
+void mq4o_qmm_f64_x32(const float* x, int64_t M, int64_t K, const uint32_t* wq,
+                      const uint16_t* scales, const uint16_t* biases, int64_t N, double* y) {
+    const int64_t G = K / MQ4O_GROUP;
+#pragma omp parallel
+    {
+        double* w = (double*)malloc((size_t)K * sizeof(double));
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < N; ++n) {
+            for (int64_t g = 0; g < G; ++g) {
+                double s = bf16_to_f32(scales[n * G + g]);
+                double b = bf16_to_f32(biases[n * G + g]);
+                for (int j = 0; j < 8; ++j) {
+                    uint32_t word = wq[n * (K / 8) + g * 8 + j];
+                    for (int p = 0; p < 8; ++p) w[g * 64 + j * 8 + p] = s * (double)((word >> (4 * p)) & 0xfu) + b;
+                }
+            }
+            for (int64_t m = 0; m < M; ++m) {
+                const float* xr = x + m * K;
+                double acc = 0.0;
+                for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * w[k];
+                y[m * N + n] = acc;
+            }
+        }
+        free(w);
     }
 }
 

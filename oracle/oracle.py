@@ -46,6 +46,7 @@ def lib():
         L.mq4o_dequantize_f64.argtypes = [P, P, P, I64, I64, P]
         L.mq4o_qmm_f64.argtypes = [P, I64, I64, P, P, P, I64, P, P]
         L.mq4o_qmm_f32.argtypes = [P, I64, I64, P, P, P, I64, P]
+        L.mq4o_qmm_f64_x32.argtypes = [P, I64, I64, P, P, P, I64, P]
         L.mq4o_qmm_mlx_bf16.argtypes = [P, I64, I64, P, P, P, I64, P]
         L.mq4o_swiglu_bf16.argtypes = [P, P, I64, P]
         L.mq4o_argmax_bf16.argtypes = [P, I64, I64, P]
@@ -212,6 +213,90 @@ def mlp_forward(x, gate, up, down):
     h = swiglu_bf16(g, u)
     _, y = qmm_f64(h, *down)
     return g, u, h, y
+
+
+# ------------------------------------- the C++ promotion reading (fp32) ---
+# In MLX's C++ API a float scalar operand is a float32 array, and a bf16 array
+# combined with a float32 one gives float32.  rms_norm (src/model/marlin.cpp:
+# 12-16) adds eps and 1.0f, so it returns float32; qmatmul (marlin.cpp:18-25)
+# then multiplies float32 activations (MLX promotes the bf16 scales and biases
+# to float32, exactly); swiglu (marlin.cpp:27-29), the residual add (:142) and
+# the lm_head logits (:161-169) are float32, and sample_token's argmax
+# (src/sampling/sampler.cpp:15) runs over float32 logits.  After the first
+# residual add the hidden state itself is float32.  These functions evaluate
+# that reading; the kernels (and the chain above) follow the bf16 activations
+# of the benchmark configurations instead.
+
+
+def qmm_f64_x32(x32, wq, s, b) -> np.ndarray:
+    """mx::quantized_matmul on float32 x in fp64 (mq4o_qmm_f64_x32): [M, N] fp64."""
+    x32 = np.ascontiguousarray(x32, dtype=np.float32)
+    if x32.ndim == 1:
+        x32 = x32[None, :]
+    M, K = x32.shape
+    N = wq.shape[0]
+    assert wq.shape == (N, K // 8) and s.shape == (N, K // GROUP) and b.shape == s.shape
+    y = np.empty((M, N), np.float64)
+    lib().mq4o_qmm_f64_x32(_p(x32), M, K, _p(np.ascontiguousarray(wq)), _p(np.ascontiguousarray(s)),
+                           _p(np.ascontiguousarray(b)), N, _p(y))
+    return y
+
+
+def rmsnorm_f32(x, w, eps: float = 1e-6) -> np.ndarray:
+    """rms_norm (src/model/marlin.cpp:12-16) in the C++ promotion reading:
+    square and mean keep the input's dtype (bf16 bits as uint16, the first
+    layer's input, or float32), "+ eps" promotes to float32, rsqrt, the
+    product with x and with (1.0f + w) are float32.  Returns float32."""
+    one = np.float32(1.0)
+    if x.dtype == np.uint16:
+        xf = bf16_to_f32(x)
+        sq = bf16_to_f32(f32_to_bf16(xf * xf))                        # square: bf16
+        sm = bf16_to_f32(f32_to_bf16(sq.sum(axis=-1, dtype=np.float32)))   # sum: bf16
+        inv = bf16_to_f32(f32_to_bf16(np.float32(1.0 / x.shape[-1])))
+        mean = bf16_to_f32(f32_to_bf16(sm * inv))                     # mean: bf16
+    else:
+        xf = np.asarray(x, np.float32)
+        mean = (xf * xf).sum(axis=-1, dtype=np.float32) * np.float32(1.0 / x.shape[-1])
+    r = one / np.sqrt(mean.astype(np.float32) + np.float32(eps))
+    return (xf * r[..., None]) * (one + bf16_to_f32(w))
+
+
+def swiglu_f32(g, u) -> np.ndarray:
+    """(sigmoid(g) * g) * u (src/model/marlin.cpp:27-29) on float32 arrays,
+    every op rounded to float32."""
+    g = np.asarray(g, np.float32)
+    sg = np.float32(1.0) / (np.float32(1.0) + np.exp(-g))
+    return (sg * g) * np.asarray(u, np.float32)
+
+
+def decode_chain_f32(x, layers, final_norm, lm, eps: float = 1e-6):
+    """The decode step's MLP halves and lm_head in the C++ promotion reading:
+    x bf16 bits [M, K]; layers a list of (norm_w, gate, up, down) with Q4
+    (wq, s, b) triples.  Returns (hidden float32 [M, K], logits float32
+    [M, N], tokens = first index of the float32 maximum)."""
+    h = np.asarray(x, np.uint16)
+    for nw, g, u, d in layers:
+        n = rmsnorm_f32(h, nw, eps)
+        gg = qmm_f64_x32(n, *g).astype(np.float32)
+        uu = qmm_f64_x32(n, *u).astype(np.float32)
+        y = qmm_f64_x32(swiglu_f32(gg, uu), *d).astype(np.float32)
+        hf = bf16_to_f32(h) if h.dtype == np.uint16 else h
+        h = hf + y
+    logits = qmm_f64_x32(rmsnorm_f32(h, final_norm, eps), *lm).astype(np.float32)
+    return h, logits, np.argmax(logits, axis=-1)
+
+
+def decode_chain_bf16(x, layers, final_norm, lm, eps: float = 1e-6):
+    """The same step with bf16 activations at every op boundary, as the
+    kernels compute it: rmsnorm_1pw, each qmm rounded once from fp64 to bf16,
+    the bf16 SwiGLU chain and residual add, argmax over bf16 logits.  Returns
+    (hidden bf16 bits, logits fp64 [M, N], tokens)."""
+    h = np.asarray(x, np.uint16)
+    for nw, g, u, d in layers:
+        _, _, _, y = mlp_forward(rmsnorm_1pw(h, nw, eps), g, u, d)
+        h = add_bf16(h, y)
+    l64, lb = qmm_f64(rmsnorm_1pw(h, final_norm, eps), *lm)
+    return h, l64, argmax_bf16(lb)
 
 
 def omp_threads() -> int:

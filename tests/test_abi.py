@@ -184,7 +184,12 @@ def test_decode_step_validation(mq4):
     assert call(inter=8192) == UNSUPPORTED
     assert call(n=33) == UNSUPPORTED
     assert call(n=-1) == UNSUPPORTED
-    assert call(vocab=0) == INVALID
+    assert call(vocab=-1) == INVALID
+    assert call(vocab=0, n=0) == INVALID                # no layers and no lm_head: nothing to do
+    assert "nothing to do" in last_error(mq4)
+    # vocab 0 runs the layers only: the final norm, lm_head and idx may be NULL,
+    # so the call passes every host check and reaches the device (absent here)
+    assert call(vocab=0, idx=None, fn=None, wq=None) == HIPERR
     assert call(vocab=(1 << 30) + 1) == INVALID
     assert call(x=None) == INVALID
     assert call(idx=None) == INVALID

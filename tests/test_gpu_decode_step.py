@@ -169,6 +169,49 @@ def test_decode_step_24_layers_against_oracle(mq4, O, dev):
     assert l64.max() - l64[tok] <= 1e-2 * lrms
 
 
+def test_decode_layers_one_launch_per_layer(mq4, dev):
+    """The per-layer mode (vocab 0): 24 launches of one MLP half each, as the
+    reference's layer loop would issue them between its attention / SSM
+    halves, give the 24-layer step's hidden state bit for bit; a 3-layer
+    launch with vocab 0 likewise; the token of the lm_head on that state
+    equals the whole step's.  The calls share one workspace (the phase tags
+    advance per call)."""
+    print("decode layers: 24 one-layer launches", flush=True)
+    layers, fnorm, lm = build_model(mq4, 24, 248320, dev)
+    step = mq4.DecodeStep(layers, fnorm, lm, EPS)
+    x = token_row(3, dev, mq4)
+    x_full = torch.empty((H,), dtype=torch.bfloat16, device=dev)
+    tok = int(step(x, x_full).item())
+    a = x.clone()
+    b = torch.empty_like(a)
+    for i in range(24):
+        step.mlp_layer(i, a, b)
+        a, b = b, a
+    xs, idx_s, _ = separate(mq4, x, layers, fnorm, lm)
+    torch.cuda.synchronize()
+    assert_same_bits(a, x_full, "24 one-layer launches")
+    assert_same_bits(xs, x_full, "separate entry points")
+    assert int(idx_s.item()) == tok
+    idx = mq4.lm_head_argmax(a.reshape(1, H), lm, norm_weight=fnorm, eps=EPS)
+    torch.cuda.synchronize()
+    assert int(idx.item()) == tok
+    three = mq4.DecodeStep(layers[:3], fnorm, lm, EPS)
+    y3 = torch.empty_like(x)
+    import ctypes
+    L = mq4.lib()
+    rc = L.mq4_decode_step(ctypes.c_void_p(x.data_ptr()), H, I, 3, ctypes.cast(three._arr, ctypes.c_void_p), None,
+                           ctypes.c_float(EPS), None, None, None, 0, None, ctypes.c_void_p(y3.data_ptr()),
+                           ctypes.c_void_p(three.workspace.data_ptr()), three.ws_bytes, None)
+    assert rc == 0
+    c = x.clone()
+    d = torch.empty_like(c)
+    for i in range(3):
+        step.mlp_layer(i, c, d)
+        c, d = d, c
+    torch.cuda.synchronize()
+    assert_same_bits(y3, c, "3-layer launch without lm_head")
+
+
 def test_decode_step_graph_replay(mq4, dev):
     """Captured once in a HIP graph and replayed with eager work in between:
     every replay gives the eager result."""
