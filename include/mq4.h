@@ -319,6 +319,33 @@ int mq4_decode_step(const uint16_t* x_in, int64_t hidden, int64_t intermediate, 
                     int64_t vocab, uint32_t* idx, uint16_t* x_out,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* The MLP half of n_layers decoder layers for M token rows (1 <= M <= 32),
+ * one launch per layer: x <- x + down(swiglu(gate n, up n)),
+ * n = rms_norm(x, norm_weight), applied layer after layer to the bf16 hidden
+ * states x_in [M, hidden]; the result lands in x_out [M, hidden].  Replaces,
+ * for M concurrent decode streams (src/core/engine.cpp:79-94), the per-layer
+ * MLP residual of src/model/marlin.cpp:141-142 (rms_norm :12-16,
+ * mlp_forward :31-35) that mq4_mlp_forward_residual computes in separate
+ * launches; same per-element arithmetic (exact (128 + q) bf16 products,
+ * fp32 sums, bf16 SwiGLU and residual), sums grouped differently.  Built for
+ * hidden = 2048 and intermediate = 6144 (other shapes return
+ * MQ4_ERR_UNSUPPORTED).  x_out must overlap neither x_in nor the workspace.
+ * Every pointer (x_in, x_out, and each layer's norm weight, packed weights,
+ * scales and biases) must be 16-byte aligned.
+ * Each launch needs 256 co-resident workgroups, so it must not overlap
+ * other work on the device.  workspace: at least
+ * mq4_mlp_layers_workspace_size(M, ...) bytes, 256-byte aligned,
+ * zero-filled once before first use and then reused by every call on the
+ * same stream (calls that overlap in time need separate workspaces; a
+ * workspace sized for M serves every smaller M).  If a launch ever times out
+ * internally (it cannot when the device runs nothing else), x_out is NaN and
+ * every later call with that workspace does the same until it is
+ * zero-filled again. */
+size_t mq4_mlp_layers_workspace_size(int64_t M, int64_t hidden, int64_t intermediate);
+int mq4_mlp_layers(const uint16_t* x_in, int64_t M, int64_t hidden, int64_t intermediate, int64_t n_layers,
+                   const mq4_mlp_layer* layers, float eps, uint16_t* x_out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* Synthetic-input generator (bench and test inputs, not a reference seam):
  * out[i] = bf16(mu + sigma * z_{offset+i}) where z is the standard-normal

@@ -33,7 +33,7 @@ __all__ = [
     "quantize_weight", "quantize_batch", "quantize_weights", "qmatmul", "mlp_gate_up_silu", "qmatmul_residual", "mlp_forward",
     "mlp_residual",
     "lm_head", "lm_head_argmax", "lm_head_last_row", "sample_token", "rms_norm", "fill_normal_bf16",
-    "DecoderLayer", "DecodeStep", "save_q4_cache", "load_q4_cache", "quantize_or_load",
+    "DecoderLayer", "DecodeStep", "BatchedMlpLayers", "save_q4_cache", "load_q4_cache", "quantize_or_load",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -118,6 +118,8 @@ def lib():
         "mq4_rms_norm": ([P, I64, I64, P, ctypes.c_float, P, P], I),
         "mq4_decode_workspace_size": ([I64, I64, I64], SZ),
         "mq4_decode_step": ([P, I64, I64, I64, P, P, ctypes.c_float, P, P, P, I64, P, P, P, SZ, P], I),
+        "mq4_mlp_layers_workspace_size": ([I64, I64, I64], SZ),
+        "mq4_mlp_layers": ([P, I64, I64, I64, I64, P, ctypes.c_float, P, P, SZ, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -653,6 +655,32 @@ class DecoderLayer:
     mlp: MLPWeights
 
 
+def _layer_array(fn: str, layers: list[DecoderLayer], H: int, I: int):
+    """The struct mq4_mlp_layer array of `layers`.  Every pointer handed to a
+    kernel is checked first: shapes and dtypes of all layers, then device and
+    contiguity."""
+    for i, ly in enumerate(layers):
+        m = ly.mlp
+        for w, k, n, name in ((m.gate_proj, H, I, "gate_proj"), (m.up_proj, H, I, "up_proj"),
+                              (m.down_proj, I, H, "down_proj")):
+            _require_quantized(w, fn)
+            if _check_weight(f"{fn} layer {i} {name}", w.weight, w.scales, w.biases, k,
+                             w.group_size, w.bits) != n:
+                raise ValueError(f"{fn}: layer {i} {name} must have {n} rows")
+        _check_vector(f"{fn} layer {i}", ly.post_attn_norm, H, "post_attn_norm")
+    arr = (_MlpLayerC * max(1, len(layers)))()
+    for i, ly in enumerate(layers):
+        m = ly.mlp
+        tensors = [(ly.post_attn_norm, "post_attn_norm")]
+        for w, name in ((m.gate_proj, "gate_proj"), (m.up_proj, "up_proj"), (m.down_proj, "down_proj")):
+            tensors += [(w.weight, f"{name}.weight"), (w.scales, f"{name}.scales"), (w.biases, f"{name}.biases")]
+        for t, tn in tensors:
+            if not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{fn}: layer {i} {tn} must be a contiguous device tensor")
+        arr[i] = _MlpLayerC(*[t.data_ptr() for t, _ in tensors])
+    return arr
+
+
 class DecodeStep:
     """One greedy decode step for one token in a single launch:
 
@@ -677,29 +705,7 @@ class DecodeStep:
         self.lm = lm
         self.eps = float(eps)
         self.intermediate = self.layers[0].mlp.gate_proj.out_features if self.layers else 6144
-        H, I = self.hidden, self.intermediate
-        # every pointer handed to the kernel is checked first: shapes and
-        # dtypes of all layers, then device and contiguity
-        for i, ly in enumerate(self.layers):
-            m = ly.mlp
-            for w, k, n, name in ((m.gate_proj, H, I, "gate_proj"), (m.up_proj, H, I, "up_proj"),
-                                  (m.down_proj, I, H, "down_proj")):
-                _require_quantized(w, fn)
-                if _check_weight(f"{fn} layer {i} {name}", w.weight, w.scales, w.biases, k,
-                                 w.group_size, w.bits) != n:
-                    raise ValueError(f"{fn}: layer {i} {name} must have {n} rows")
-            _check_vector(f"{fn} layer {i}", ly.post_attn_norm, H, "post_attn_norm")
-        arr = (_MlpLayerC * max(1, len(self.layers)))()
-        for i, ly in enumerate(self.layers):
-            m = ly.mlp
-            tensors = [(ly.post_attn_norm, "post_attn_norm")]
-            for w, name in ((m.gate_proj, "gate_proj"), (m.up_proj, "up_proj"), (m.down_proj, "down_proj")):
-                tensors += [(w.weight, f"{name}.weight"), (w.scales, f"{name}.scales"), (w.biases, f"{name}.biases")]
-            for t, tn in tensors:
-                if not t.is_cuda or not t.is_contiguous():
-                    raise ValueError(f"{fn}: layer {i} {tn} must be a contiguous device tensor")
-            arr[i] = _MlpLayerC(*[t.data_ptr() for t, _ in tensors])
-        self._arr = arr
+        self._arr = _layer_array(fn, self.layers, self.hidden, self.intermediate)
         self.final_norm = _need(final_norm, torch.bfloat16, "final_norm")
         for t, tn in ((lm.weight, "weight"), (lm.scales, "scales"), (lm.biases, "biases")):
             if not t.is_cuda or not t.is_contiguous():
@@ -757,6 +763,73 @@ class DecodeStep:
                                      None, None, None, 0, None, _ptr(x_out), _ptr(self.workspace), self.ws_bytes,
                                      _stream(x.device)))
         return x_out
+
+
+class BatchedMlpLayers:
+    """The MLP halves of a stack of decoder layers for M token rows
+    (1 <= M <= max_rows <= 32), one launch per layer:
+
+        for layer in layers:  x = x + mlp_forward(rms_norm(x, layer.post_attn_norm))
+
+    i.e. src/model/marlin.cpp:141-142 for M concurrent decode streams
+    (src/core/engine.cpp:79-94), through mq4_mlp_layers.  Same per-element
+    arithmetic as mlp_residual (bf16 x (128 + q) products, fp32 sums, bf16
+    SwiGLU and residual) with the sums grouped differently, so results agree
+    with it to fp32 rounding, not bit for bit.  Holds its workspace
+    (zero-filled once here); calls are stream-ordered and must not overlap
+    other device work.  Built for hidden 2048 / intermediate 6144."""
+
+    def __init__(self, layers: list[DecoderLayer], max_rows: int = 32, eps: float = 1e-6):
+        fn = "BatchedMlpLayers"
+        if not layers:
+            raise ValueError(f"{fn}: needs at least one layer")
+        self.layers = list(layers)
+        self.hidden = self.layers[0].mlp.gate_proj.in_features
+        self.intermediate = self.layers[0].mlp.gate_proj.out_features
+        self.eps = float(eps)
+        self._arr = _layer_array(fn, self.layers, self.hidden, self.intermediate)
+        L = lib()
+        self.max_rows = int(max_rows)
+        self.ws_bytes = L.mq4_mlp_layers_workspace_size(self.max_rows, self.hidden, self.intermediate)
+        if self.ws_bytes == 0:
+            raise NotImplementedError(
+                f"{fn}: built for hidden 2048, intermediate 6144 and 1..32 rows "
+                f"(got {self.hidden}, {self.intermediate}, max_rows {max_rows})")
+        dev = self.layers[0].post_attn_norm.device
+        self.workspace = torch.zeros(self.ws_bytes, dtype=torch.uint8, device=dev)
+
+    def reset(self) -> None:
+        """Zero the workspace (clears the sticky error state)."""
+        self.workspace.zero_()
+
+    def _run(self, fn: str, x: torch.Tensor, x_out, first: int, count: int) -> torch.Tensor:
+        x = _need(x, torch.bfloat16, "x")
+        if x.dim() != 2 or x.shape[1] != self.hidden or not 1 <= x.shape[0] <= self.max_rows:
+            raise ValueError(f"{fn}: x must be [M, {self.hidden}] with 1 <= M <= {self.max_rows}")
+        if x_out is None:
+            x_out = torch.empty_like(x)
+        elif (not isinstance(x_out, torch.Tensor) or x_out.dtype != torch.bfloat16 or x_out.shape != x.shape
+              or not x_out.is_contiguous()):
+            raise ValueError(f"{fn}: x_out must be a contiguous bf16 tensor shaped like x")
+        layer_ptr = ctypes.c_void_p(ctypes.addressof(self._arr) + first * ctypes.sizeof(_MlpLayerC))
+        _check(lib().mq4_mlp_layers(_ptr(x), x.shape[0], self.hidden, self.intermediate, count, layer_ptr,
+                                    self.eps, _ptr(x_out), _ptr(self.workspace), self.ws_bytes,
+                                    _stream(x.device)))
+        return x_out
+
+    def __call__(self, x: torch.Tensor, x_out: torch.Tensor | None = None) -> torch.Tensor:
+        """x: bf16 [M, hidden]; returns the hidden states after every layer
+        (x_out, if given, receives them and must not overlap x)."""
+        return self._run("BatchedMlpLayers", x, x_out, 0, len(self.layers))
+
+    def layer(self, i: int, x: torch.Tensor, x_out: torch.Tensor | None = None) -> torch.Tensor:
+        """x + mlp_forward(rms_norm(x, layers[i].post_attn_norm)) for the M rows
+        of x in one launch: the MLP half the reference's layer loop runs
+        between its attention / SSM halves, for callers that interleave other
+        work per layer.  x_out must not overlap x."""
+        if not 0 <= i < len(self.layers):
+            raise IndexError(f"BatchedMlpLayers.layer: layer {i} of {len(self.layers)}")
+        return self._run("BatchedMlpLayers.layer", x, x_out, i, 1)
 
 
 # on-disk Q4 weight cache (safetensors, MLX naming): see q4cache.py

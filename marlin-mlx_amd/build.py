@@ -44,8 +44,13 @@ CFLAGS = [
 # work on the MFMA results; with them in AGPRs every group moved 128 values
 # between AGPRs and VGPRs (v_accvgpr_read/write), half the loop's VALU
 # instructions.
+# mq4_rows.hip: no wave-level atomic combining.  Its one arrival count per
+# workgroup would otherwise be rewritten into a combined add whose result is
+# read back at once, which stalls the issuing wave on every load issued
+# before it (the count's result is only needed at the end of the kernel).
 EXTRA_FLAGS = {
     "mq4_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "mq4_rows.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 
 # Sources whose kernels wait for their LDS DMA with exact vmcnt counts: that

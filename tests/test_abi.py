@@ -257,3 +257,60 @@ def test_mlp_residual_workspace_and_validation(mq4):
     assert call(fake(A16), need, M=0) == INVALID
     assert call(fake(A16), need, y=None) == INVALID
     assert call(fake(A16), need, x=fake(A16 + 2)) == ALIGN
+
+
+def test_mlp_layers_validation(mq4):
+    """mq4_mlp_layers (the batched one-launch MLP half): the workspace size
+    (control words, the h and part-sum exchange words sized for 32 rows, two
+    ping-pong hidden states of M rows) and every rejection before the first
+    HIP call."""
+    L = mq4.lib()
+    up = lambda v: (v + 255) // 256 * 256
+    ws_size = L.mq4_mlp_layers_workspace_size
+    for bad in ((0, 2048, 6144), (33, 2048, 6144), (4, 4096, 6144), (4, 2048, 8192)):
+        assert ws_size(*bad) == 0
+    exch = 256 + up(8 * 32 * 384 * 8) + up(8 * 32 * 64 * 32 * 8)
+    for M in (1, 16, 32):
+        assert ws_size(M, 2048, 6144) == exch + 2 * up(M * 2048 * 2)
+    sizes = [ws_size(m, 2048, 6144) for m in range(1, 33)]
+    assert all(b >= a for a, b in zip(sizes, sizes[1:]))
+    need = ws_size(16, 2048, 6144)
+    good = _Layer(*([A16] * 10))
+    arr = (_Layer * 2)(good, good)
+    WS = 0x4000000
+
+    def call(**kw):
+        return L.mq4_mlp_layers(
+            kw.get("x", fake(A16)), kw.get("M", 16), kw.get("hidden", 2048), kw.get("inter", 6144),
+            kw.get("n", 2), kw.get("layers", ctypes.cast(arr, ctypes.c_void_p)), 1e-6,
+            kw.get("xo", fake(0x200000)), kw.get("ws", fake(WS)), kw.get("wsb", need), S)
+
+    assert call(hidden=4096) == UNSUPPORTED
+    assert "hidden" in last_error(mq4)
+    assert call(inter=8192) == UNSUPPORTED
+    assert call(M=0) == UNSUPPORTED
+    assert call(M=33) == UNSUPPORTED
+    assert call(n=0) == INVALID
+    assert call(x=None) == INVALID
+    assert call(xo=None) == INVALID
+    assert call(layers=None) == INVALID
+    assert call(x=fake(A16 + 2)) == ALIGN
+    assert call(xo=fake(0x200000 + 8)) == ALIGN
+    assert call(xo=fake(A16 + 16 * 2048)) == INVALID           # overlaps the last row of x
+    assert "overlap" in last_error(mq4)
+    assert call(xo=fake(A16 + 16 * 2048 * 2)) == HIPERR         # adjacent: passes the host checks
+    assert call(ws=None) == WORKSPACE
+    assert call(wsb=need - 1) == WORKSPACE
+    assert call(M=32) == WORKSPACE                              # a 16-row workspace is too small for 32
+    assert call(ws=fake(WS + 128)) == WORKSPACE
+    assert call(xo=fake(WS + need - 16)) == INVALID             # inside the workspace
+    bad = (_Layer * 2)(good, _Layer(*([A16] * 9 + [0])))
+    assert call(layers=ctypes.cast(bad, ctypes.c_void_p)) == INVALID
+    assert "layer 1" in last_error(mq4)
+    mis = (_Layer * 2)(good, _Layer(*([A16, A16 + 8] + [A16] * 8)))
+    assert call(layers=ctypes.cast(mis, ctypes.c_void_p)) == ALIGN
+    mis = (_Layer * 2)(_Layer(*([A16] * 8 + [A16 + 8, A16])), good)   # down scales: 16-byte loads
+    assert call(layers=ctypes.cast(mis, ctypes.c_void_p)) == ALIGN
+    # every host check passed: the call reaches the device query (absent here)
+    assert call() == HIPERR
+    assert call(M=8) == HIPERR                                  # a larger workspace serves fewer rows
