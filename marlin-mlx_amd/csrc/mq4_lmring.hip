@@ -1,0 +1,271 @@
+// Batched lm_head + argmax with a weight ring, gfx950: for M token rows
+// (1 <= M <= 32) at K = 2048,
+//
+//   logits = lm_head(rms_norm(x, w)),   idx[m] = argmax(logits[m])
+//
+// (src/model/marlin.cpp:145, 161-169; src/sampling/sampler.cpp:14-16) with
+// exactly the arithmetic of the MFMA GEMV's argmax epilogue in mq4_mfma.hip:
+// K split over 8 waves of 4 groups each, the per-group fold
+// acc = s * P' + (c * X + acc) on exact bf16 x (128 + q) MFMA products, the
+// wave partials summed in wave order, one bf16 rounding per logit, the
+// (bf16 key, lowest index) argmax.  Logits and tokens are bit-identical to it.
+//
+// What differs is the weight stream.  One persistent 8-wave workgroup per CU
+// walks the 16-row tiles blockIdx.x, blockIdx.x + gridDim.x, ...; each wave
+// keeps kR tiles of its 128-byte line per row in flight, staged into LDS by
+// DMA as whole lines (about 100 KB per CU in flight, the bytes the HBM
+// latency needs), where the GEMV holds one tile in registers.  Per tile the
+// eight wave partials meet in LDS (double-buffered, one barrier per tile)
+// and wave (tile % 8) sums them, rounds and updates its running argmax.
+#include "mq4_device.h"
+#include "mq4_gemv.h"
+#include "mq4_host.h"
+#include "mq4_mfma_ops.h"
+#include "mq4_stage.h"
+
+namespace mq4 {
+namespace lmr {
+
+using stage::dma16;
+using stage::dma4;
+using stage::stage_chunk;
+using stage::stage_slot;
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int K = 2048;
+constexpr int GA = K / 64;            // groups per row (32)
+constexpr int GWA = GA / kWaves;      // groups per wave (4)
+constexpr int kR = 6;                 // tiles in flight per wave
+constexpr int kDmaPerTile = 3;        // two 1 KB line blocks + one scale/bias block
+constexpr int kMaxM = 32;
+
+struct Params {
+    const uint16_t* x;         // [M, K] bf16
+    const uint16_t* norm;      // [K] (1 + w) RMSNorm weight (NORM)
+    float eps;
+    QMat A;                    // [N, K] Q4
+    int M, N;
+    uint16_t* y;               // [M, N] bf16 logits, or null
+    uint64_t* partial;         // [M][kPartialStride] per-workgroup best keys
+};
+
+struct alignas(16) Smem {
+    uint4 w[kWaves][kR][2][64];            // each wave's line blocks, rows 0-7 and 8-15 (96 KB)
+    uint32_t sb[kWaves][kR][64];           // each wave's scales (dwords 0-31) and biases (32-63)
+    mf::f32x4_t red[2][kWaves][2][64];     // wave partials, double-buffered by tile parity
+    float ss[kWaves][kMaxM];
+    uint64_t best[kWaves][kMaxM];
+};
+
+template <int N>
+__device__ __forceinline__ void wait_tiles_after(int n) {
+    // at most n later tiles (kDmaPerTile DMA each) may stay in flight
+    static_assert(N == kR - 1, "ring depth");
+    switch (n) {
+        case 5: wait_vmcnt<5 * kDmaPerTile>(); break;
+        case 4: wait_vmcnt<4 * kDmaPerTile>(); break;
+        case 3: wait_vmcnt<3 * kDmaPerTile>(); break;
+        case 2: wait_vmcnt<2 * kDmaPerTile>(); break;
+        case 1: wait_vmcnt<1 * kDmaPerTile>(); break;
+        default: wait_vmcnt<0>(); break;
+    }
+}
+
+template <int MT, bool NORM>
+__global__ __launch_bounds__(kThreads) void lm_ring_kernel(Params p) {
+#pragma clang fp contract(off)
+    __shared__ Smem sm;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c16 = lane & 15, kq = lane >> 4;
+    const int M = p.M, N = p.N, g0 = wave * GWA;
+    const int ntiles = (N + 15) / 16;
+    const int T = (int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+
+    // ---- activations and norm weights (tracked loads, waited for before any DMA) ----
+    uint4 xa[MT][GWA][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + c16;
+        const int mm = m < M ? m : M - 1;              // rows >= M repeat row M - 1, never read back
+#pragma unroll
+        for (int gi = 0; gi < GWA; ++gi) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.x + (int64_t)mm * K + 64 * (g0 + gi) + 16 * kq);
+            xa[mt][gi][0] = src[0];
+            xa[mt][gi][1] = src[1];
+        }
+    }
+    uint4 nwv[GWA][2];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int gi = 0; gi < GWA; ++gi) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.norm + 64 * (g0 + gi) + 16 * kq);
+            nwv[gi][0] = src[0];
+            nwv[gi][1] = src[1];
+        }
+        // sums of squares: this lane's 16 values per group, the four k blocks
+        // of the wave, then the 8 waves in wave order (as the MFMA GEMV)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            float s = 0.0f;
+#pragma unroll
+            for (int gi = 0; gi < GWA; ++gi) {
+                mf::sumsq4(s, xa[mt][gi][0]);
+                mf::sumsq4(s, xa[mt][gi][1]);
+            }
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            if (kq == 0) sm.ss[wave][16 * mt + c16] = s;
+        }
+    }
+    wait_vmcnt<0>();
+
+    // ---- the ring: tile j of this workgroup -> slot j % kR ----
+    auto issue = [&](int j, int slot) {
+        const int n0 = 16 * ((int)blockIdx.x + j * (int)gridDim.x);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int sl = 64 * b + lane, row = sl >> 3, u = stage_chunk(sl, row);
+            const int n = n0 + row < N ? n0 + row : N - 1;     // rows past N repeat row N - 1, never used
+            dma16(p.A.wq + (int64_t)n * (K / 8) + 32 * wave + 4 * u, &sm.w[wave][slot][b][0]);
+        }
+        const int r = (lane & 31) >> 1, n = n0 + r < N ? n0 + r : N - 1;
+        const uint16_t* src = lane < 32 ? p.A.s : p.A.b;
+        dma4(src + (int64_t)n * GA + GWA * wave + 2 * (lane & 1), &sm.sb[wave][slot][0]);
+    };
+#pragma unroll
+    for (int j = 0; j < kR; ++j)
+        if (j < T) issue(j, j);
+    lds_barrier();                                     // sums of squares
+
+    // ---- normalized, pair-ordered activations and their group sums ----
+    const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+    const mf::f32x4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    mf::f32x4_t X[MT][GWA];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (NORM) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) tot += sm.ss[w][16 * mt + c16];
+            const float r = rms_inv(tot, K, p.eps);
+#pragma unroll
+            for (int gi = 0; gi < GWA; ++gi)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint4 v = xa[mt][gi][h], w = nwv[gi][h];
+                    xa[mt][gi][h] = make_uint4(norm_word(v.x, w.x, r), norm_word(v.y, w.y, r), norm_word(v.z, w.z, r),
+                                               norm_word(v.w, w.w, r));
+                }
+        }
+#pragma unroll
+        for (int gi = 0; gi < GWA; ++gi) {
+            xa[mt][gi][0] = mf::pair_order(xa[mt][gi][0]);
+            xa[mt][gi][1] = mf::pair_order(xa[mt][gi][1]);
+            X[mt][gi] = mf::mfma16(xa[mt][gi][1], ones, mf::mfma16(xa[mt][gi][0], ones, zero4));
+        }
+    }
+
+    // Each tile's 16 x 16 MT outputs are summed by all eight waves, 32 MT
+    // each: thread t of wave v takes output i = t % 4 of partial lane
+    // l = 8 v + (t % 32) / 4 of tile mt = t / 32, i.e. row
+    // m = 16 mt + 4 (v / 2) + i of column c = l % 16 (fixed across tiles).
+    const bool red_on = lane < 32 * MT;
+    const int r_mt = lane >> 5, r_l = 8 * wave + ((lane & 31) >> 2), r_i = lane & 3;
+    const int r_m = 16 * r_mt + 4 * (r_l >> 4) + r_i, r_c = r_l & 15;
+    uint64_t best = 0;
+
+    for (int j = 0; j < T; ++j) {
+        const int slot = j % kR;
+        wait_tiles_after<kR - 1>(T - 1 - j < kR - 1 ? T - 1 - j : kR - 1);
+        mf::f32x4_t acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = zero4;
+        const uint2* wl = reinterpret_cast<const uint2*>(&sm.w[wave][slot][0][0]);
+        const uint32_t* sbl = &sm.sb[wave][slot][0];
+#pragma unroll
+        for (int gi = 0; gi < GWA; ++gi) {
+            const uint2 wv = wl[2 * stage_slot(c16, c16, 2 * gi + (kq >> 1)) + (kq & 1)];
+            const uint4 b0 = mf::unpack_word(wv.x), b1 = mf::unpack_word(wv.y);
+            const uint32_t sw = sbl[2 * c16 + (gi >> 1)], bw = sbl[32 + 2 * c16 + (gi >> 1)];
+            const float s = bf16_to_f32((gi & 1) ? (sw >> 16) : (sw & 0xffffu));
+            const float c = affine_c(s, (gi & 1) ? (bw >> 16) : (bw & 0xffffu));
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const mf::f32x4_t P = mf::mfma16(xa[mt][gi][1], b1, mf::mfma16(xa[mt][gi][0], b0, zero4));
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[mt][i] = __builtin_fmaf(s, P[i], __builtin_fmaf(c, X[mt][gi][i], acc[mt][i]));
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) sm.red[j & 1][wave][mt][lane] = acc[mt];
+        lds_barrier();                                 // this tile's partials; this wave's slot reads done
+        if (j + kR < T) issue(j + kR, slot);
+        if (red_on) {
+            // the 8 partials in wave order, one bf16 rounding, the running argmax
+            const float* rp = reinterpret_cast<const float*>(&sm.red[j & 1][0][r_mt][r_l]) + r_i;
+            constexpr int kStride = 2 * 64 * 4;            // floats from one wave's partials to the next
+            float v = rp[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) v += rp[w * kStride];
+            const int n = 16 * ((int)blockIdx.x + j * (int)gridDim.x) + r_c;
+            if (r_m < M && n < N) {
+                const uint32_t lb = f32_to_bf16(v);
+                if (p.y) p.y[(int64_t)r_m * N + n] = (uint16_t)lb;
+                const uint64_t key = argmax_key(lb, (uint32_t)n);
+                best = key > best ? key : best;
+            }
+        }
+    }
+
+    // ---- per-workgroup best key of each row: the 8 columns of a wave's
+    // threads (t = 32 mt + 4 a + i, a = 0..7), then the two waves v, v ^ 1 ----
+    uint64_t b = best;
+#pragma unroll
+    for (int off = 4; off < 32; off <<= 1) {
+        const uint64_t o = shfl_xor_u64(b, off);
+        b = o > b ? o : b;
+    }
+    if (red_on && (lane & 28) == 0) sm.best[wave][r_m] = b;
+    __syncthreads();
+    if (tid < M) {
+        // rows 16 mt + 4 (v / 2) + i are held by waves v = 2 (m % 16 / 4) and v + 1
+        const int v0 = 2 * ((tid & 15) >> 2);
+        const uint64_t b0 = sm.best[v0][tid], b1 = sm.best[v0 + 1][tid];
+        p.partial[(int64_t)tid * kPartialStride + blockIdx.x] = b1 > b0 ? b1 : b0;
+    }
+}
+
+}  // namespace lmr
+
+int launch_lm_ring(const GemvParams& a, bool norm, hipStream_t st) {
+    if (a.K != lmr::K || a.m_valid < 1 || a.m_valid > lmr::kMaxM || a.N < 1 || !a.partial || !a.idx) return -1;
+    if (!aligned(a.x, 16) || !aligned(a.A.wq, 16) || !aligned(a.A.s, 4) || !aligned(a.A.b, 4)) return -1;
+    if (norm && !aligned(a.norm_w, 16)) return -1;
+    const int ntiles = (a.N + 15) / 16;
+    int grid = num_cus();
+    if (grid > ntiles) grid = ntiles;
+    if (grid > kPartialStride) grid = kPartialStride;
+    lmr::Params p{};
+    p.x = a.x;
+    p.norm = a.norm_w;
+    p.eps = a.eps;
+    p.A = a.A;
+    p.M = a.m_valid;
+    p.N = a.N;
+    p.y = a.y;
+    p.partial = a.partial;
+    const dim3 g((unsigned)grid), b(lmr::kThreads);
+    if (a.m_valid <= 16) {
+        if (norm) hipLaunchKernelGGL((lmr::lm_ring_kernel<1, true>), g, b, 0, st, p);
+        else hipLaunchKernelGGL((lmr::lm_ring_kernel<1, false>), g, b, 0, st, p);
+    } else {
+        if (norm) hipLaunchKernelGGL((lmr::lm_ring_kernel<2, true>), g, b, 0, st, p);
+        else hipLaunchKernelGGL((lmr::lm_ring_kernel<2, false>), g, b, 0, st, p);
+    }
+    launch_argmax_finalize(a.partial, grid, a.m_valid, a.idx, st);
+    return 0;
+}
+
+}  // namespace mq4

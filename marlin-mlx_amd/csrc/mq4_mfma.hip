@@ -521,7 +521,11 @@ int launch_q4_mfma_gemv(const GemvParams& a, int epi, bool norm, hipStream_t st)
         case EPI_STORE_F32: rc = norm ? -1 : dispatch<EPI_STORE_F32, false>(a, st); break;
         case EPI_RESIDUAL: rc = norm ? -1 : dispatch<EPI_RESIDUAL, false>(a, st); break;
         case EPI_SWIGLU: rc = norm ? dispatch<EPI_SWIGLU, true>(a, st) : dispatch<EPI_SWIGLU, false>(a, st); break;
-        case EPI_ARGMAX: rc = norm ? dispatch<EPI_ARGMAX, true>(a, st) : dispatch<EPI_ARGMAX, false>(a, st); break;
+        case EPI_ARGMAX:
+            // K = 2048 (the model's lm_head): the weight-ring kernel, same arithmetic
+            rc = launch_lm_ring(a, norm, st);
+            if (rc != 0) rc = norm ? dispatch<EPI_ARGMAX, true>(a, st) : dispatch<EPI_ARGMAX, false>(a, st);
+            break;
         default: rc = -1;
     }
     return rc;

@@ -45,12 +45,18 @@
 #include "mq4_device.h"
 #include "mq4_host.h"
 #include "mq4_mfma_ops.h"
+#include "mq4_stage.h"
 
 #include <mutex>
 
 namespace mq4 {
 
 namespace rows {
+
+using stage::dma16;
+using stage::dma4;
+using stage::stage_chunk;
+using stage::stage_slot;
 
 constexpr int kNWG = 256;            // workgroups (one per CU)
 constexpr int kWaves = 8;
@@ -99,36 +105,6 @@ __device__ __forceinline__ bool errored(const uint32_t* ctrl) {
     return __hip_atomic_load(ctrl + 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
 }
 __device__ __forceinline__ uint32_t tag_of(uint64_t w) { return (uint32_t)(w >> 32); }
-
-// Weight lines staged by LDS DMA: one DMA instruction moves 64 lanes x 16
-// bytes, eight lanes per 128-byte line (whole lines, the pattern that keeps
-// the CU's load pipeline busy for the fewest cycles).  Within a line the
-// eight 16-byte chunks go to the lanes rotated by (row / 2) % 8, so that the
-// MFMA operand reads (16 rows x one chunk at a time) hit 16 distinct bank
-// groups.  Line index G (row, or row + 16 x line-in-row) and chunk u live at
-// 16-byte slot 8 G + ((u - (row >> 1)) & 7) of the staging buffer.
-// LDS DMA issued as inline assembly, so that the compiler does not track
-// it: it would otherwise wait for every outstanding DMA of the wave before
-// each LDS access.  The kernel waits for its DMA itself (wait_vmcnt), before
-// the reads of the staged data and before the barriers after which other
-// waves read it; the compiler's own waits for the activation loads, issued
-// before any DMA, stay correct (an untracked later load only makes a
-// wait for an earlier one stricter).  M0 holds the wave-uniform LDS
-// destination; lane l writes bytes [size l, size (l + 1)) of it.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-__device__ __forceinline__ void dma16(const void* src, const void* lds_dst) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_dst))) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* src, const void* lds_dst) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-                 :: "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_dst))) : "memory", "m0");
-}
-
-__device__ __forceinline__ int stage_slot(int G, int row, int u) { return 8 * G + ((u - (row >> 1)) & 7); }
-__device__ __forceinline__ int stage_chunk(int slot, int row) { return ((slot & 7) + (row >> 1)) & 7; }
 
 constexpr int kDmaA = 2 * RA * 128 / 1024;   // gate/up DMA instructions per wave (6)
 constexpr int kDmaB = 16 * (IX / 2) / 1024;  // down DMA blocks per tile (6: 16 rows x 384 bytes)
@@ -196,24 +172,10 @@ __global__ __launch_bounds__(kThreads) void mlp_rows_kernel(Params p) {
         err = __hip_atomic_load(p.ctrl + 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // ---- loads: activations, then norm weights, scales and biases (the
-    // weight lines follow once the sums of squares are in LDS) ----
-    // activations of the wave's groups (MFMA A layout: row m = 16 mt + c16,
-    // k block kq).  Rows m >= M repeat row M - 1: an MFMA output row depends
-    // on its own A row only, and those rows are never read back.
+    // ---- loads, in this order: norm weights, scales and biases and this
+    // wave's gate/up weight lines (LDS DMA), then the activations; the down
+    // weight lines follow once the sums of squares are in LDS ----
     const int g0 = wave * GWA;
-    uint4 xa[MT][GWA][2];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = 16 * mt + c16;
-        const int mm = m < M ? m : M - 1;
-#pragma unroll
-        for (int gi = 0; gi < GWA; ++gi) {
-            const uint4* src = reinterpret_cast<const uint4*>(p.x + (int64_t)mm * H + 64 * (g0 + gi) + 16 * kq);
-            xa[mt][gi][0] = src[0];
-            xa[mt][gi][1] = src[1];
-        }
-    }
     // norm weights, scales and biases by LDS DMA, lane-linear: norm 16-byte
     // chunk 64 w + lane (waves 0-3); gate/up scales and biases [gate s | up s
     // | gate b | up b] of the 24 rows, 16-byte chunk 64 w + lane (waves 0-5);
@@ -234,6 +196,32 @@ __global__ __launch_bounds__(kThreads) void mlp_rows_kernel(Params p) {
                  reinterpret_cast<uint32_t*>(&sm.sdn[0][0]) + 128 * wave + 64 * i);
         }
     }
+    // gate/up weight lines: the wave's 128 bytes (groups 4 w .. 4 w + 3) of
+    // the 48 rows [24 gate; 24 up], block i holding rows 8 i .. 8 i + 7
+#pragma unroll
+    for (int i = 0; i < kDmaA; ++i) {
+        const int slot = 64 * i + lane, row = slot >> 3, u = stage_chunk(slot, row);
+        const uint32_t* wq = row < RA ? p.gate.wq : p.up.wq;
+        const int grow = xj * IX + rk * RA + (row < RA ? row : row - RA);
+        dma16(wq + (int64_t)grow * (H / 8) + 32 * wave + 4 * u, &sm.u.wgu[wave][i][0]);
+    }
+    // activations of the wave's groups (MFMA A layout: row m = 16 mt + c16,
+    // k block kq), issued after the DMA above: loads complete in issue
+    // order, so once the activations are in, so are the staged lines.  Rows
+    // m >= M repeat row M - 1: an MFMA output row depends on its own A row
+    // only, and those rows are never read back.
+    uint4 xa[MT][GWA][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + c16;
+        const int mm = m < M ? m : M - 1;
+#pragma unroll
+        for (int gi = 0; gi < GWA; ++gi) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.x + (int64_t)mm * H + 64 * (g0 + gi) + 16 * kq);
+            xa[mt][gi][0] = src[0];
+            xa[mt][gi][1] = src[1];
+        }
+    }
     // ---- sums of squares of the M rows (this wave's 256 k) ----
     // (the error word is read later; a workgroup that starts on a set error
     // word skips its work, but every workgroup computes this much first)
@@ -249,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void mlp_rows_kernel(Params p) {
         s += __shfl_xor(s, 32);
         if (kq == 0) sm.ss[wave][16 * mt + c16] = s;
     }
-    wait_vmcnt<0>();                                   // the norm, scale and bias DMA of this wave
+    wait_vmcnt<0>();                                   // this wave's DMA so far (read after B1)
     if (tid == 0) {
         // e sits in a register (its load has returned) before the count below
         // is issued, so no workgroup can read an epoch the count moves on
@@ -259,15 +247,6 @@ __global__ __launch_bounds__(kThreads) void mlp_rows_kernel(Params p) {
         // count this workgroup in; the 256th arrival (all have read the
         // epoch) moves the epoch on for the next launch, at its end
         arrived = __hip_atomic_fetch_add(p.ctrl + 16, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // gate/up weight lines: the wave's 128 bytes (groups 4 w .. 4 w + 3) of
-    // the 48 rows [24 gate; 24 up], block i holding rows 8 i .. 8 i + 7
-#pragma unroll
-    for (int i = 0; i < kDmaA; ++i) {
-        const int slot = 64 * i + lane, row = slot >> 3, u = stage_chunk(slot, row);
-        const uint32_t* wq = row < RA ? p.gate.wq : p.up.wq;
-        const int grow = xj * IX + rk * RA + (row < RA ? row : row - RA);
-        dma16(wq + (int64_t)grow * (H / 8) + 32 * wave + 4 * u, &sm.u.wgu[wave][i][0]);
     }
     // down weight lines: tile tb = wave / 2 (rows 64 r + 16 tb + [0, 16)),
     // part xj (384 bytes of each row, three lines); the tile's two waves
@@ -309,7 +288,6 @@ __global__ __launch_bounds__(kThreads) void mlp_rows_kernel(Params p) {
             for (int t = 0; t < NTA; ++t) acc[t][mt] = zero4;
         }
         // ---- gate/up products over the wave's 4 groups ----
-        wait_vmcnt<kDmaB / 2>();                       // this wave's gate/up lines have landed
 #pragma unroll
         for (int gi = 0; gi < GWA; ++gi) {
             mf::f32x4_t X[MT];
