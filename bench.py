@@ -758,7 +758,8 @@ def bench_batched(E, layers, lm, norm_w, layer_norms):
                        "separate_entries_us": round(us_sep, 1), "one_call_mlp_us": round(us_one, 1),
                        "one_launch_mlp_us": round(us_lay, 1), "one_launch_tokens_agree": round(agree, 3)}
     return {"workload": "M rows x [24 x (RMSNorm + gate/up 6144x2048 + SwiGLU, down 2048x6144 + residual), "
-                        "RMSNorm + lm_head 248320x2048 + argmax]; MFMA GEMV (M >= 5) / dot2 GEMV (M <= 4)",
+                        "RMSNorm + lm_head 248320x2048 + argmax]; MLP halves: MFMA GEMV (M >= 5) / dot2 GEMV "
+                        "(M <= 4) or mq4_mlp_layers; lm_head + argmax: weight-ring kernel (M >= 3)",
             "note": "us_per_step is the fastest of three call structures, all HIP graphs of the same "
                     "per-element arithmetic: separate entries (mq4_rmsnorm_gate_up_silu + mq4_qmm_residual per "
                     "layer), one mq4_mlp_residual call per layer (the greedy tokens of these two must agree), "

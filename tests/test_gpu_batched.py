@@ -208,3 +208,25 @@ def test_lm_head_ring_equals_mfma_gemv(mq4, O, dev, lm, M, N):
     got = idx.cpu().numpy().astype(np.uint32)
     assert np.array_equal(got, O.argmax_bf16(lg))
     assert np.array_equal(idx2.cpu().numpy().astype(np.uint32), got)
+
+
+@pytest.mark.parametrize("M", [3, 4])
+def test_lm_head_ring_small_m_rows_independent(mq4, O, dev, lm, M):
+    """From 3 rows the lm_head + argmax takes the weight-ring kernel, whose
+    rows are independent (16-row MFMA tiles, rows past M repeat the last
+    one): the logits of M rows equal the first M rows of a 5-row call bit for
+    bit (5 rows: pinned to the MFMA GEMV above), and against the oracle they
+    meet the lm_head bars."""
+    print(f"lm_head ring rows: M={M}", flush=True)
+    qt, qh = lm
+    x5 = mq4.fill_normal_bf16((5, H), 3500, 0.0, 2.0, device=dev)
+    nw = mq4.fill_normal_bf16((H,), 2002, 0.1, 0.02, device=dev)
+    idx, lg = mq4.lm_head_argmax(x5[:M].contiguous(), qt, return_logits=True, norm_weight=nw, eps=1e-6)
+    idx5, lg5 = mq4.lm_head_argmax(x5, qt, return_logits=True, norm_weight=nw, eps=1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host_u16(lg), to_host_u16(lg5)[:M])
+    assert np.array_equal(idx.cpu().numpy(), idx5.cpu().numpy()[:M])
+    hn = O.rmsnorm_1pw(to_host_u16(x5[:M]), to_host_u16(nw), 1e-6)
+    ref64, refb = O.qmm_f64(hn, *qh)
+    ulp = O.bf16_ulp_diff(to_host_u16(lg), refb)
+    assert np.mean(ulp == 0) >= 0.98
