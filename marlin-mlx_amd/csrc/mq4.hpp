@@ -237,6 +237,54 @@ private:
     int64_t max_rows_;
 };
 
+// The MLP halves of a layer stack for M concurrent token rows (1 <= M <=
+// max_rows <= 32), one launch per layer (mq4_mlp_layers; src/model/
+// marlin.cpp:141-142 for M streams, src/core/engine.cpp:79-94): holds the
+// layer table and its workspace, zero-filled here once.  x_out must overlap
+// neither x nor the workspace; results agree with MlpResidual to fp32
+// rounding.  Built for hidden 2048 / intermediate 6144.
+class BatchedMlpLayers {
+public:
+    struct Layer {
+        const uint16_t* post_attn_norm;
+        const MLPWeights* mlp;
+    };
+    BatchedMlpLayers(const std::vector<Layer>& layers, int64_t max_rows)
+        : ws_(mq4_mlp_layers_workspace_size(max_rows, 2048, 6144)), max_rows_(max_rows) {
+        for (const Layer& l : layers) {
+            const MLPWeights& w = *l.mlp;
+            table_.push_back(mq4_mlp_layer{l.post_attn_norm, w.gate_proj.wq(), w.gate_proj.s(), w.gate_proj.b(),
+                                           w.up_proj.wq(), w.up_proj.s(), w.up_proj.b(), w.down_proj.wq(),
+                                           w.down_proj.s(), w.down_proj.b()});
+            mlps_.push_back(l.mlp);
+        }
+        if (ws_.get() && hipMemset(ws_.get(), 0, ws_.bytes()) != hipSuccess) ws_.reset();
+    }
+    // layers [first, first + count) of the table over the M rows of x
+    Result<int> operator()(const uint16_t* x, int64_t M, float eps, uint16_t* x_out, hipStream_t stream,
+                           size_t first = 0, size_t count = SIZE_MAX) {
+        if (!ws_.get()) return Error{MQ4_ERR_WORKSPACE, "BatchedMlpLayers: no workspace (unsupported sizes?)"};
+        if (M > max_rows_) return Error{MQ4_ERR_WORKSPACE, "BatchedMlpLayers: M exceeds max_rows"};
+        if (first >= table_.size()) return Error{MQ4_ERR_INVALID_ARG, "BatchedMlpLayers: no such layer"};
+        if (count > table_.size() - first) count = table_.size() - first;
+        for (size_t l = first; l < first + count; ++l) {
+            const MLPWeights& w = *mlps_[l];
+            if (auto r = check_q4("BatchedMlpLayers", {&w.gate_proj, &w.up_proj, &w.down_proj}); !r) return r.error();
+        }
+        if (M == 0) return 0;
+        const int rc = mq4_mlp_layers(x, M, 2048, 6144, (int64_t)count, table_.data() + first, eps, x_out, ws_.get(),
+                                      ws_.bytes(), stream);
+        if (rc != MQ4_OK) return last_error(rc);
+        return 0;
+    }
+
+private:
+    DeviceBuffer ws_;
+    int64_t max_rows_;
+    std::vector<mq4_mlp_layer> table_;
+    std::vector<const MLPWeights*> mlps_;
+};
+
 // Greedy next token(s): idx[m] = argmax(lm_head(rms_norm(hidden))) for each
 // of the M rows (src/model/marlin.cpp:145, 161-169; src/sampling/sampler.cpp:14-16).
 class GreedyLmHead {

@@ -161,6 +161,51 @@ int main(int argc, char** argv) {
         rejected = rejected && !r3 && r3.error().code == MQ4_ERR_UNSUPPORTED;
     }
     std::printf("format_rejected %d\n", rejected ? 1 : 0);
+
+    // mq4::BatchedMlpLayers (one launch per layer, hidden 2048 / intermediate
+    // 6144): two layers over 16 rows as one call equal the two one-layer
+    // calls chained by the caller, bit for bit; more rows than the workspace
+    // was sized for are refused
+    bool batched_ok = true;
+    {
+        const int64_t BH = 2048, BI = 6144, R = 16;
+        std::vector<mq4::DeviceBuffer> braw;
+        std::vector<mq4::WeightView> bviews;
+        std::vector<mq4::MLPWeights> bl(2);
+        std::vector<mq4::DeviceBuffer> bnorm;
+        for (int l = 0; l < 2; ++l) {
+            const int64_t shp[3][2] = {{BI, BH}, {BI, BH}, {BH, BI}};
+            for (int q = 0; q < 3; ++q) {
+                braw.emplace_back((size_t)(2 * shp[q][0] * shp[q][1]));
+                if (fill(braw.back().as<uint16_t>(), shp[q][0] * shp[q][1], 5000 + 3 * l + q, 0.0, 0.02, st)) return 3;
+                bviews.push_back({braw.back().as<uint16_t>(), shp[q][0], shp[q][1]});
+            }
+            bnorm.emplace_back(2 * BH);
+            if (fill(bnorm.back().as<uint16_t>(), BH, 5100 + l, 0.1, 0.02, st)) return 3;
+        }
+        auto qs = mq4::quantize_weights(bviews, st);
+        CHECK(qs);
+        for (int l = 0; l < 2; ++l) {
+            bl[l].gate_proj = std::move(qs.value()[3 * l]);
+            bl[l].up_proj = std::move(qs.value()[3 * l + 1]);
+            bl[l].down_proj = std::move(qs.value()[3 * l + 2]);
+        }
+        mq4::BatchedMlpLayers stack({{bnorm[0].as<uint16_t>(), &bl[0]}, {bnorm[1].as<uint16_t>(), &bl[1]}}, R);
+        mq4::DeviceBuffer x0(2 * R * BH), x1(2 * R * BH), x2(2 * R * BH), xs(2 * R * BH);
+        if (fill(x0.as<uint16_t>(), R * BH, 5200, 0.0, 1.0, st)) return 3;
+        CHECK(stack(x0.as<uint16_t>(), R, 1e-6f, xs.as<uint16_t>(), st));               // both layers
+        CHECK(stack(x0.as<uint16_t>(), R, 1e-6f, x1.as<uint16_t>(), st, 0, 1));         // layer 0
+        CHECK(stack(x1.as<uint16_t>(), R, 1e-6f, x2.as<uint16_t>(), st, 1, 1));         // layer 1
+        if (hipStreamSynchronize(st) != hipSuccess) return 4;
+        std::vector<uint16_t> a(R * BH), b(R * BH);
+        if (hipMemcpy(a.data(), xs.get(), 2 * R * BH, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(b.data(), x2.get(), 2 * R * BH, hipMemcpyDeviceToHost) != hipSuccess)
+            return 4;
+        batched_ok = a == b;
+        auto over = stack(x0.as<uint16_t>(), R + 1, 1e-6f, xs.as<uint16_t>(), st);
+        batched_ok = batched_ok && !over && over.error().code == MQ4_ERR_WORKSPACE;
+    }
+    std::printf("batched_layers_ok %d\n", batched_ok ? 1 : 0);
     (void)hipStreamDestroy(st);
     return 0;
 }

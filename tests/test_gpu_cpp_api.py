@@ -55,3 +55,5 @@ def test_cpp_demo_matches_python_binding(mq4, O, dev):
     assert lines[5] == "mlp_residual_rows_ok 1"
     # tensors of another format are refused by the fused mirrors
     assert lines[6] == "format_rejected 1"
+    # mq4::BatchedMlpLayers: a two-layer call equals two chained one-layer calls
+    assert lines[7] == "batched_layers_ok 1"
