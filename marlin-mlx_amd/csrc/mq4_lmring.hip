@@ -1,5 +1,5 @@
 // Batched lm_head + argmax with a weight ring, gfx950: for M token rows
-// (1 <= M <= 32) at K = 2048,
+// (3 <= M <= 32) at K = 2048,
 //
 //   logits = lm_head(rms_norm(x, w)),   idx[m] = argmax(logits[m])
 //
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void lm_ring_kernel(Params p) {
 }  // namespace lmr
 
 int launch_lm_ring(const GemvParams& a, bool norm, hipStream_t st) {
-    if (a.K != lmr::K || a.m_valid < 1 || a.m_valid > lmr::kMaxM || a.N < 1 || !a.partial || !a.idx) return -1;
+    if (a.K != lmr::K || a.m_valid < 3 || a.m_valid > lmr::kMaxM || a.N < 1 || !a.partial || !a.idx) return -1;
     if (!aligned(a.x, 16) || !aligned(a.A.wq, 16) || !aligned(a.A.s, 4) || !aligned(a.A.b, 4)) return -1;
     if (norm && !aligned(a.norm_w, 16)) return -1;
     const int ntiles = (a.N + 15) / 16;

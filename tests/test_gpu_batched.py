@@ -187,14 +187,17 @@ def test_batched_edge_shapes(mq4, O, dev, case):
         check_close(O, lg, y64, f"edge {case}")
 
 
-@pytest.mark.parametrize("M,N", [(5, V), (16, V), (17, V), (32, V), (16, 1000), (20, 4097), (8, 17)])
+@pytest.mark.parametrize("M,N", [(1, V), (2, V), (1, 17), (2, 4097), (5, V), (16, V), (17, V), (32, V),
+                                 (16, 1000), (20, 4097), (8, 17)])
 def test_lm_head_ring_equals_mfma_gemv(mq4, O, dev, lm, M, N):
     """From 5 rows at K = 2048 the lm_head + argmax runs as the weight-ring
     kernel (mq4_lmring.hip): the MFMA GEMV's arithmetic (8 waves x 4 groups,
     wave partials in wave order), so its logits equal, bit for bit, the MFMA
-    GEMV's plain product (qmatmul, the same K split and order), and the
-    tokens are the argmax of those logits.  Ragged N: fewer tiles than
-    workgroups (1000 and 17 rows) and a last tile of one row (4097)."""
+    GEMV's plain product (qmatmul, the same K split and order); 1-2 rows run
+    the dot2 GEMV, whose plain product is the same kernel with another
+    epilogue.  The tokens are the argmax of those logits.  Ragged N: fewer
+    tiles than workgroups (1000 and 17 rows) and a last tile of one row
+    (4097)."""
     print(f"lm_head ring vs MFMA GEMV: M={M} N={N}", flush=True)
     qt = lm[0] if N == V else mq4.quantize_weight(
         mq4.fill_normal_bf16((N, H), 7100 + N, 0.0, 0.02, device=dev))
