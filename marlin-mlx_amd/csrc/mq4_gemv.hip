@@ -509,11 +509,10 @@ static int run_gemv(const GemvParams& base, int M, hipStream_t st) {
 // where the MFMA kernel does not cover K.
 template <int EPI, bool NORM>
 static int run_small(const GemvParams& base, int M, hipStream_t st) {
-    // the lm_head + argmax from 3 rows: the weight-ring kernel (the MFMA
-    // GEMV's arithmetic) outruns the dot2 GEMV, which reads the 254 MB once
-    // per 4 rows at dot2 rate; 1-2 rows stay on the dot2 GEMV (a dot2 copy of
-    // the ring measured slower there: 49.9 against 47.9 us at one row)
-    if (EPI == EPI_ARGMAX && M >= 3 && M < kMfmaMinM && launch_lm_ring(base, NORM, st) == 0) return 0;
+    // the lm_head + argmax at K = 2048: the weight-ring kernels (1-2 rows
+    // with the dot2 GEMV's arithmetic, 3-4 with the MFMA GEMV's, which
+    // outruns the dot2 GEMV reading the 254 MB once per 4 rows at dot2 rate)
+    if (EPI == EPI_ARGMAX && M < kMfmaMinM && launch_lm_ring(base, NORM, st) == 0) return 0;
     if (M < kMfmaMinM) return run_gemv<EPI, NORM>(base, M, st);
     for (int m0 = 0; m0 < M; m0 += kMfmaMaxM) {
         const int mc = (M - m0) < kMfmaMaxM ? (M - m0) : kMfmaMaxM;

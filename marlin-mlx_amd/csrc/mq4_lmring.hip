@@ -1,5 +1,5 @@
 // Batched lm_head + argmax with a weight ring, gfx950: for M token rows
-// (3 <= M <= 32) at K = 2048,
+// (1 <= M <= 32) at K = 2048,
 //
 //   logits = lm_head(rms_norm(x, w)),   idx[m] = argmax(logits[m])
 //
@@ -239,8 +239,174 @@ __global__ __launch_bounds__(kThreads) void lm_ring_kernel(Params p) {
 
 }  // namespace lmr
 
+// ---- 1-2 rows: the dot2 GEMV's arithmetic through the same kind of ring ----
+//
+// The dot2 GEMV (mq4_gemv.hip, K = 2048: one 16-byte slice per lane, 4 rows
+// per iteration, no K split) forms each logit as: per lane, the dot2 chain
+// of its slice's 4 words, the group fold s * D + c * X added to 0, then
+// wave_multi_reduce over the 64 lanes.  This kernel forms every logit the
+// same way (so logits and tokens are bit-identical to it, and the one-launch
+// decode step, which reproduces the dot2 GEMV, keeps its token) but feeds it
+// differently: each of 16 waves per CU streams its own 4-row batches with
+// two batches in flight, a 1 KB row per DMA instruction (lane l receives
+// slice l), and the four rows' scales and biases as two contiguous 256-byte
+// runs.  Every DMA takes a scalar base and a constant per-lane offset, so no
+// vector instruction goes to addressing; the waves meet only at the end.
+namespace lmd {
+
+constexpr int kWaves = 16;
+constexpr int kThreads = 64 * kWaves;
+constexpr int K = 2048;
+constexpr int RPI = 4;                 // rows per batch (the dot2 GEMV's)
+constexpr int kRD = 2;                 // batches in flight per wave
+constexpr int kDmaPerBatch = RPI + 2;
+
+struct alignas(16) Smem {
+    uint4 w[kWaves][kRD][RPI][64];     // row r of a batch: lane l's slice l (128 KB)
+    uint32_t sb[kWaves][kRD][2][64];   // scales, then biases, of the 4 rows (16 dwords per row)
+    uint64_t best[kWaves][2];
+};
+
+template <int M, bool NORM>
+__global__ __launch_bounds__(kThreads) void lm_ring_dot2_kernel(lmr::Params p) {
+#pragma clang fp contract(off)
+    constexpr int V = RPI * M;
+    constexpr int SH = 6 - log2_const<V>();
+    __shared__ Smem sm;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int N = p.N;                                 // a multiple of RPI (checked by the host)
+    const int nb = N / RPI;
+    const int gw = (int)blockIdx.x * kWaves + wave, W = (int)gridDim.x * kWaves;
+    const int T = gw < nb ? (nb - 1 - gw) / W + 1 : 0;
+    const char* wq = reinterpret_cast<const char*>(p.A.wq);
+    const char* sq = reinterpret_cast<const char*>(p.A.s);
+    const char* bq = reinterpret_cast<const char*>(p.A.b);
+
+    auto issue = [&](int j, int slot) {
+        const int64_t r0 = (int64_t)RPI * (gw + j * W);
+#pragma unroll
+        for (int r = 0; r < RPI; ++r)
+            stage::dma16_s(wq + (r0 + r) * (K / 2), 16u * lane, &sm.w[wave][slot][r][0]);
+        stage::dma4_s(sq + r0 * (K / 32), 4u * lane, &sm.sb[wave][slot][0][0]);
+        stage::dma4_s(bq + r0 * (K / 32), 4u * lane, &sm.sb[wave][slot][1][0]);
+    };
+#pragma unroll
+    for (int j = 0; j < kRD; ++j)
+        if (j < T) issue(j, j);
+
+    // ---- this lane's slice of the activations (tracked loads issued after
+    // the DMA: loads complete in issue order, so they arrive with it) ----
+    uint4 xv[M][4];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) xv[m][w] = reinterpret_cast<const uint4*>(p.x + (int64_t)m * K)[lane * 4 + w];
+    if constexpr (NORM) {
+        uint4 wn[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) wn[w] = reinterpret_cast<const uint4*>(p.norm)[lane * 4 + w];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint4 a = xv[m][w];
+                s = sumsq_word(s, a.x);
+                s = sumsq_word(s, a.y);
+                s = sumsq_word(s, a.z);
+                s = sumsq_word(s, a.w);
+            }
+            const float r = rms_inv(wave_sum(s), K, p.eps);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint4 e = xv[m][w];
+                xv[m][w] = make_uint4(norm_word(e.x, wn[w].x, r), norm_word(e.y, wn[w].y, r),
+                                      norm_word(e.z, wn[w].z, r), norm_word(e.w, wn[w].w, r));
+            }
+        }
+    }
+    uint32_t xp[M][16];
+    float xs[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) sum = pair_chunk(xv[m][w], &xp[m][4 * w], sum);
+        xs[m] = sum;
+    }
+
+    uint64_t best = 0;
+    const int sbw = lane >> 2, sbh = (lane >> 1) & 1;  // dword and half of this slice's group (lane / 2)
+    for (int j = 0; j < T; ++j) {
+        const int slot = j % kRD;
+        static_assert(kRD == 2, "one later batch may stay in flight");
+        if (j + 1 < T) wait_vmcnt<kDmaPerBatch>();
+        else wait_vmcnt<0>();
+        float acc[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPI; ++r) {
+            const uint4 wv = sm.w[wave][slot][r][lane];
+            const uint32_t sw = sm.sb[wave][slot][0][16 * r + sbw], bw = sm.sb[wave][slot][1][16 * r + sbw];
+            const uint32_t sbits = sbh ? (sw >> 16) : (sw & 0xffffu), bbits = sbh ? (bw >> 16) : (bw & 0xffffu);
+            float d[M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) d[m] = 0.0f;
+            const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t p0 = nib_pair_bf16<0>(wd[w]);
+                const uint32_t p1 = nib_pair_bf16<1>(wd[w]);
+                const uint32_t p2 = nib_pair_bf16<2>(wd[w]);
+                const uint32_t p3 = nib_pair_bf16<3>(wd[w]);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    d[m] = dot2_bf16(xp[m][4 * w + 0], p0, d[m]);
+                    d[m] = dot2_bf16(xp[m][4 * w + 1], p1, d[m]);
+                    d[m] = dot2_bf16(xp[m][4 * w + 2], p2, d[m]);
+                    d[m] = dot2_bf16(xp[m][4 * w + 3], p3, d[m]);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[r * M + m] += affine_term(sbits, bbits, d[m], xs[m]);
+        }
+        // every read of this slot is done before its refill is issued
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (j + kRD < T) issue(j + kRD, slot);
+        const float val = wave_multi_reduce<V>(acc, lane);
+        const int vidx = lane >> SH, m = vidx % M, row = RPI * (gw + j * W) + vidx / M;
+        if ((lane & ((1 << SH) - 1)) == 0 && m < p.M) {
+            const uint32_t lb = f32_to_bf16(val);
+            if (p.y) p.y[(int64_t)m * N + row] = (uint16_t)lb;
+            const uint64_t key = argmax_key(lb, (uint32_t)row);
+            best = key > best ? key : best;
+        }
+    }
+    // ---- per-workgroup best key of each row: lanes of the same m (lane bit
+    // SH holds m for M = 2), then the waves ----
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        if (M == 2 && off == (1 << SH)) continue;
+        const uint64_t o = shfl_xor_u64(best, off);
+        best = o > best ? o : best;
+    }
+    if (lane < (M << SH) && (lane & ((1 << SH) - 1)) == 0) sm.best[wave][lane >> SH] = best;
+    __syncthreads();
+    if (tid < p.M) {
+        uint64_t b = sm.best[0][tid];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) b = sm.best[w][tid] > b ? sm.best[w][tid] : b;
+        p.partial[(int64_t)tid * kPartialStride + blockIdx.x] = b;
+    }
+}
+
+}  // namespace lmd
+
 int launch_lm_ring(const GemvParams& a, bool norm, hipStream_t st) {
-    if (a.K != lmr::K || a.m_valid < 3 || a.m_valid > lmr::kMaxM || a.N < 1 || !a.partial || !a.idx) return -1;
+    if (a.K != lmr::K || a.m_valid < 1 || a.m_valid > lmr::kMaxM || a.N < 1 || !a.partial || !a.idx) return -1;
+    if (a.m_valid <= 2 && a.N % lmd::RPI != 0) return -1;   // the 1-2 row kernel reads whole 4-row batches
     if (!aligned(a.x, 16) || !aligned(a.A.wq, 16) || !aligned(a.A.s, 4) || !aligned(a.A.b, 4)) return -1;
     if (norm && !aligned(a.norm_w, 16)) return -1;
     const int ntiles = (a.N + 15) / 16;
@@ -257,7 +423,16 @@ int launch_lm_ring(const GemvParams& a, bool norm, hipStream_t st) {
     p.y = a.y;
     p.partial = a.partial;
     const dim3 g((unsigned)grid), b(lmr::kThreads);
-    if (a.m_valid <= 16) {
+    if (a.m_valid <= 2) {
+        const dim3 bd(lmd::kThreads);
+        if (a.m_valid == 1) {
+            if (norm) hipLaunchKernelGGL((lmd::lm_ring_dot2_kernel<1, true>), g, bd, 0, st, p);
+            else hipLaunchKernelGGL((lmd::lm_ring_dot2_kernel<1, false>), g, bd, 0, st, p);
+        } else {
+            if (norm) hipLaunchKernelGGL((lmd::lm_ring_dot2_kernel<2, true>), g, bd, 0, st, p);
+            else hipLaunchKernelGGL((lmd::lm_ring_dot2_kernel<2, false>), g, bd, 0, st, p);
+        }
+    } else if (a.m_valid <= 16) {
         if (norm) hipLaunchKernelGGL((lmr::lm_ring_kernel<1, true>), g, b, 0, st, p);
         else hipLaunchKernelGGL((lmr::lm_ring_kernel<1, false>), g, b, 0, st, p);
     } else {

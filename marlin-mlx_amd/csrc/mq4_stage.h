@@ -38,6 +38,18 @@ __device__ __forceinline__ void dma4(const void* src, const void* lds_dst) {
                  :: "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr(lds_dst))) : "memory");
 }
 
+// The same DMA with a wave-uniform 64-bit base in scalar registers and a
+// 32-bit per-lane byte offset (the saddr form): no vector address arithmetic
+// per instruction.  `base` must be wave-uniform.
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t voff, const void* lds_dst) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr(lds_dst))) : "memory");
+}
+__device__ __forceinline__ void dma4_s(const void* base, uint32_t voff, const void* lds_dst) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 :: "v"(voff), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr(lds_dst))) : "memory");
+}
+
 __device__ __forceinline__ int stage_slot(int G, int row, int u) { return 8 * G + ((u - (row >> 1)) & 7); }
 __device__ __forceinline__ int stage_chunk(int slot, int row) { return ((slot & 7) + (row >> 1)) & 7; }
 
