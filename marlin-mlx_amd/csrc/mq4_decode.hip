@@ -40,6 +40,7 @@
 
 #include "mq4_device.h"
 #include "mq4_host.h"
+#include "mq4_stage.h"
 
 namespace mq4 {
 
@@ -190,27 +191,27 @@ __device__ __forceinline__ float pairs_d(const uint32_t* pr, const uint32_t* xp)
     return d;
 }
 
-// Normalize xraw (H bf16) with (1 + w) RMSNorm and build xp/xs.  Every I/O
-// wave computes the full sum of squares (lane l sums the 16 words of slice l,
-// then the wave reduces: the order of the separate kernels) and handles a
-// quarter of the slices, 4 lanes per slice, one 16-byte chunk per lane; nw is
-// this lane's chunk of the norm weight, loaded a layer ahead.
-__device__ void stage_norm_x(Smem& sm, const uint4 nw, float eps, int io, int lane) {
+// (1 + w) RMSNorm of x into xp/xs.  Every I/O wave computes the full sum of
+// squares (lane l sums the 16 words of slice l, then the wave reduces: the
+// order of the separate kernels) and handles a quarter of the slices, 4 lanes
+// per slice, one 16-byte chunk per lane (chunk io*64 + lane of x); nw is this
+// lane's chunk of the norm weight, loaded a layer ahead.
+__device__ __forceinline__ float norm_rinv(const uint4 (&v)[4], float eps) {
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint4 v = reinterpret_cast<const uint4*>(sm.xraw)[lane * 4 + k];
-        ss = sumsq_word(ss, v.x);
-        ss = sumsq_word(ss, v.y);
-        ss = sumsq_word(ss, v.z);
-        ss = sumsq_word(ss, v.w);
+        ss = sumsq_word(ss, v[k].x);
+        ss = sumsq_word(ss, v[k].y);
+        ss = sumsq_word(ss, v[k].z);
+        ss = sumsq_word(ss, v[k].w);
     }
     ss = wave_sum(ss);
-    const float r = rms_inv(ss, H, eps);
+    return rms_inv(ss, H, eps);
+}
+__device__ __forceinline__ void norm_chunk(Smem& sm, const uint4 nw, float r, const uint4 xv, int io, int lane) {
     constexpr int SPW = SA / kNIO;                 // 16 slices per I/O wave
     const int sl = io * SPW + (lane >> 2);
     const int q = lane & 3;
-    const uint4 xv = reinterpret_cast<const uint4*>(sm.xraw)[sl * 4 + q];
     const uint4 xn = make_uint4(norm_word(xv.x, nw.x, r), norm_word(xv.y, nw.y, r), norm_word(xv.z, nw.z, r),
                                 norm_word(xv.w, nw.w, r));
     uint32_t pr[4];
@@ -218,6 +219,12 @@ __device__ void stage_norm_x(Smem& sm, const uint4 nw, float eps, int io, int la
     sm.xp[q][sl] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
     const float c1 = quad_lane<1>(c), c2 = quad_lane<2>(c), c3 = quad_lane<3>(c);
     if (q == 0) sm.xs[sl] = ((c + c1) + c2) + c3;
+}
+// The same from x in xraw (all I/O waves' quarters, after a barrier).
+__device__ void stage_norm_x(Smem& sm, const uint4 nw, float eps, int io, int lane) {
+    const uint4* x4 = reinterpret_cast<const uint4*>(sm.xraw);
+    const uint4 v[4] = {x4[lane * 4], x4[lane * 4 + 1], x4[lane * 4 + 2], x4[lane * 4 + 3]};
+    norm_chunk(sm, nw, norm_rinv(v, eps), x4[io * 64 + lane], io, lane);
 }
 
 // Pair the polled h (this wave's quarter of the slices): 4 lanes per slice,
@@ -246,19 +253,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
     const int wg = blockIdx.x;
     const int L = p.n_layers;
 
-    if (threadIdx.x == 0) {
-        sm.epoch = __hip_atomic_load(p.ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sm.abort = errored(p.ctrl) ? 1 : 0;
-    }
-    __syncthreads();
-    const uint32_t base = sm.epoch * 128u + 1u;  // phase tags base + [0, 2*layers+1]: never 0, disjoint per call
-    if (sm.abort) {
-        if (wg == 0 && threadIdx.x == 0 && p.vocab > 0) p.idx[0] = 0xffffffffu;
-        return;
-    }
-
-    // LDS DMA of one layer's weights into compute wave c's staging buffers
-    // (issued by the I/O waves, see below).
+    // LDS DMA of one layer's weights into compute wave c's staging buffers.
     const int sdw = lane < 48 ? lane : 47;           // dword of a 192-byte scale/bias run
     auto dmaA = [&](int c, int l, int t) {           // kDmaA / 2 instructions (t: 0 gate, 1 up)
         const Layer& Ly = p.layers[l];
@@ -289,11 +284,67 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(Q.b + (int64_t)rowB * (I / 64)) + sdw,
                                          &wsb[c].b[0], 4, 0, 0);
     };
+    // The same for layer 0 at the start of the launch, issued as inline
+    // assembly that the compiler does not track (it would otherwise wait for
+    // every outstanding DMA of the wave before its next LDS read); the
+    // issuing wave waits for them itself by exact counts.
+    auto dmaA0 = [&](int c, int t) {                 // kDmaA / 2 instructions
+        const QMat& Q = t == 0 ? p.layers[0].gate : p.layers[0].up;
+        const int rowA = wg * (I / kNWG) + c * RA;
+#pragma unroll
+        for (int r = 0; r < RA; ++r)
+            stage::dma16(reinterpret_cast<const uint4*>(Q.wq + (int64_t)(rowA + r) * (H / 8)) + lane,
+                         &wsa[c].w[t][r][0]);
+        stage::dma4(reinterpret_cast<const uint32_t*>(Q.s + (int64_t)rowA * (H / 64)) + sdw, &wsa[c].s[t][0]);
+        stage::dma4(reinterpret_cast<const uint32_t*>(Q.b + (int64_t)rowA * (H / 64)) + sdw, &wsa[c].b[t][0]);
+    };
+    auto dmaB0 = [&](int c) {                        // kDmaB instructions
+        const QMat& D = p.layers[0].down;
+        const int rowB = wg * (H / kNWG) + c * RB;
+#pragma unroll
+        for (int j = 0; j < SPL_B; ++j)
+            stage::dma16(reinterpret_cast<const uint4*>(D.wq + (int64_t)rowB * (I / 8)) + j * 64 + lane, &wsb[c].w[j][0]);
+        stage::dma4(reinterpret_cast<const uint32_t*>(D.s + (int64_t)rowB * (I / 64)) + sdw, &wsb[c].s[0]);
+        stage::dma4(reinterpret_cast<const uint32_t*>(D.b + (int64_t)rowB * (I / 64)) + sdw, &wsb[c].b[0]);
+    };
     static_assert(kNCW == 2 * kNIO, "each I/O wave stages the weights of two compute waves");
     static_assert(kDmaA % 2 == 0, "gate and up halves");
 
+    // Layer 0 starts as early as the launch allows.  The I/O waves load x and
+    // the first norm weight before any weight DMA is issued in this CU (a
+    // CU's loads return in issue order: one issued behind a layer's 83 KB of
+    // weights waits for all of them), and thread 0 reads the epoch and the
+    // error word meanwhile.  Right after B0 each compute wave DMAs its
+    // layer-0 gate and up rows (issue is paced by HBM: about 2 us for a CU's
+    // 55 KB), and unpacks the gate rows as soon as they land; the I/O waves
+    // normalize x and then DMA the down rows.  The epoch and the error word
+    // are first read after B1 (an aborted launch leaves there), so the
+    // weight stream starts before the epoch is known.  (The two roles branch
+    // apart before their first loads, so that the compiler's waits for the
+    // I/O waves' loads do not reach the compute waves' code.)
+    const int io = wave;                             // I/O wave index (wave < kNIO)
+    // this lane's 16-byte chunk of a norm weight (slice io*16 + lane/4,
+    // chunk lane%4), loaded one layer ahead of its use
+    const int nchunk = (io * (SA / kNIO) + (lane >> 2)) * 4 + (lane & 3);
+    auto norm_of = [&](int l) { return l < L ? p.layers[l].norm : p.final_norm; };
     if (wave < kNIO) {
         // ============================ I/O waves ============================
+        uint4 nw = reinterpret_cast<const uint4*>(norm_of(0))[nchunk];    // L > 0 or vocab > 0
+        const uint4* x4 = reinterpret_cast<const uint4*>(p.x_in);
+        const uint4 xv = x4[io * 64 + lane];        // chunk io*64 + lane of x
+        uint4 xa[4];                                 // slice `lane` of x (16 words)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xa[k] = x4[lane * 4 + k];
+        // (read by every lane: a load in a one-lane branch is awaited at the
+        // branch's end, which would hold B0 until the loads above return)
+        const uint32_t epoch0 = __hip_atomic_load(p.ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t err0 = __hip_atomic_load(p.ctrl + 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds_barrier();                               // B0: x, norm and epoch loads issued
+        if (threadIdx.x == 0) {                      // read by every wave after B1
+            sm.epoch = epoch0;
+            sm.abort = err0 != 0u ? 1 : 0;
+        }
+        uint32_t base = 0;  // phase tags base + [0, 2*layers+1]: never 0, disjoint per call (set after B1)
         // Weights reach the compute waves' LDS staging buffers by DMA, issued
         // only in phases without a poll in flight (weight traffic ahead of a
         // poll in the CU's memory pipeline delays it) and by waves idle in
@@ -302,49 +353,39 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         //   gate rows of layer l+1: each compute wave, RMSNorm phase of l;
         //   up rows of layer l+1:   I/O waves, gate/up phase of l, waited by B5;
         //   down row of layer l+1:  I/O waves, down phase of l, waited by B3 of l+1.
+        // Layer 0: see above.
         // I/O wave io serves compute waves 2*io and 2*io+1.  The barriers
         // carry no memory fence (lds_barrier): a fence would wait for all
         // outstanding DMA.
-        const int io = wave;
-        // this lane's 16-byte chunk of a norm weight (slice io*16 + lane/4,
-        // chunk lane%4), loaded one layer ahead of its use
-        const int nchunk = (io * (SA / kNIO) + (lane >> 2)) * 4 + (lane & 3);
-        auto norm_of = [&](int l) { return l < L ? p.layers[l].norm : p.final_norm; };
-        uint4 nw = reinterpret_cast<const uint4*>(norm_of(0))[nchunk];    // L > 0 or vocab > 0
         // the copy of the exchange buffers this workgroup reads
         const uint64_t* xcopy = p.xbuf + (size_t)(wg % kCopies) * (H / 2);
         const uint64_t* hcopy = p.hbuf + (size_t)(wg % kCopies) * (I / 2);
         constexpr int kIoA = kDmaA, kIoB = 2 * kDmaB;   // up halves of two waves; two down rows
-        if (L > 0) {
-            dmaA(2 * io, 0, 0);
-            dmaA(2 * io, 0, 1);
-            dmaA(2 * io + 1, 0, 0);
-            dmaA(2 * io + 1, 0, 1);
-            dmaB(2 * io, 0);
-            dmaB(2 * io + 1, 0);
-            wait_vmcnt<kIoB>();
+        // layer 0: x into xraw (the residual) and its RMSNorm straight from
+        // the registers, while the weights are still streaming in
+        *reinterpret_cast<uint4*>(&sm.xraw[io * (H / 2 / kNIO) + lane * 4]) = xv;
+        if (L == 0 && wg == 0 && p.x_out) {
+            uint32_t* xo = reinterpret_cast<uint32_t*>(p.x_out) + io * (H / 2 / kNIO) + lane * 4;
+            xo[0] = xv.x, xo[1] = xv.y, xo[2] = xv.z, xo[3] = xv.w;
         }
-        lds_barrier();                                         // B0: gate/up weights of layer 0 staged
+        norm_chunk(sm, nw, norm_rinv(xa, p.eps), xv, io, lane);
+        if (L > 0) {                                 // layer 0's down rows, waited before B3
+            dmaB0(2 * io);
+            dmaB0(2 * io + 1);
+        }
         for (int l = 0; l <= L; ++l) {
-            // layers only: the last layer's x words (and x_out) are written;
-            // nothing reads them in this launch
+            // layers only: the last layer's x_out is written; nothing reads
+            // x words in this launch after it
             if (l == L && p.vocab == 0) break;
-            // ---- x of layer l (the input at l == 0) -> xraw ----
-            if (l == 0) {
-#pragma unroll
-                for (int i = 0; i < H / 2 / kNIO / 64; ++i) {
-                    const int word = io * (H / 2 / kNIO) + i * 64 + lane;
-                    const uint32_t v = reinterpret_cast<const uint32_t*>(p.x_in)[word];
-                    sm.xraw[word] = v;
-                    if (L == 0 && wg == 0 && p.x_out) reinterpret_cast<uint32_t*>(p.x_out)[word] = v;
-                }
-            } else if (!poll_words<H / 2 / kNIO>(xcopy + io * (H / 2 / kNIO), base + 2 * l,
-                                                 sm.xraw + io * (H / 2 / kNIO), p, lane)) {
+            // ---- x of layer l > 0 -> xraw (layer 0's was stored above) ----
+            if (l > 0 && !poll_words<H / 2 / kNIO>(xcopy + io * (H / 2 / kNIO), base + 2 * l,
+                                                   sm.xraw + io * (H / 2 / kNIO), p, lane)) {
                 sm.abort = 1;
             }
             lds_barrier();                                     // B1: xraw complete
             if (sm.abort) break;
-            stage_norm_x(sm, nw, p.eps, io, lane);
+            if (l == 0) base = sm.epoch * 128u + 1u;
+            if (l > 0) stage_norm_x(sm, nw, p.eps, io, lane);
             lds_barrier();                                     // B2: xp/xs ready
             if (l == L) break;
             if (l + 1 < L || p.vocab > 0) nw = reinterpret_cast<const uint4*>(norm_of(l + 1))[nchunk];
@@ -387,13 +428,16 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
                 wait_vmcnt<kIoB>();                            // up weights of layer l+1 staged
             }
             lds_barrier();                                     // B5: new x rows in sm.out
-            {   // this workgroup's new x words into every copy
+            {   // this workgroup's new x words into every copy (layers only:
+                // not after the last layer, whose words nothing reads)
                 constexpr int XW = H / kNWG / 2;
                 const int i = io * 64 + lane;
                 if (i < XW * kCopies) {
                     const int c = i / XW, w = i - c * XW;
                     const uint32_t v = sm.out[2 * w] | (sm.out[2 * w + 1] << 16);
-                    st_tagged(p.xbuf + (size_t)c * (H / 2) + wg * XW + w, ((uint64_t)(base + 2 * l + 2) << 32) | v);
+                    if (p.vocab > 0 || l + 1 < L)
+                        st_tagged(p.xbuf + (size_t)c * (H / 2) + wg * XW + w,
+                                  ((uint64_t)(base + 2 * l + 2) << 32) | v);
                     if (c == 0 && l == L - 1 && p.x_out) reinterpret_cast<uint32_t*>(p.x_out)[wg * XW + w] = v;
                 }
             }
@@ -440,12 +484,19 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
 
     // ============================ compute waves ============================
     const int cw = wave - kNIO;
-    // This wave's weights arrive in its LDS staging buffers by DMA (issued
-    // and awaited by the I/O waves, no registers held while in flight) and
-    // are unpacked into bf16 nibble pairs while the activations are being
-    // exchanged: gate/up weights of layer l after B5 of layer l-1, down
-    // weights after B3.  The compute waves issue no memory operation inside
-    // the layer loop, so their barriers carry no fence (lds_barrier).
+    lds_barrier();                                   // B0
+    if (L > 0) {
+        dmaA0(cw, 0);
+        dmaA0(cw, 1);
+    }
+    // This wave's weights arrive in its LDS staging buffers by DMA (no
+    // registers held while in flight): its gate rows by its own DMA (layer 0:
+    // gate and up rows, issued right after B0), the other rows by the I/O
+    // waves.  They are unpacked into bf16 nibble pairs while the activations
+    // are being exchanged: gate/up weights of layer l after B5 of layer l-1,
+    // down weights after B3.  The compute waves' only memory operations are
+    // their own DMAs, awaited by vmcnt, so their barriers carry no fence
+    // (lds_barrier).
     WStageA& SA_ = wsa[cw];
     WStageB& SB_ = wsb[cw];
     const int rowB = wg * (H / kNWG) + cw * RB;     // down row of this wave
@@ -453,30 +504,26 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
 
     uint32_t pa[2][RA][16];
     float ks_a[2][RA], kc_a[2][RA];
-    auto unpackA = [&]() {
+    auto unpackA = [&](int t) {                      // t: 0 gate, 1 up
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < RA; ++r) {
-                const uint4 w = SA_.w[t][r][lane];
-                nib_pairs(w.x, &pa[t][r][0]);
-                nib_pairs(w.y, &pa[t][r][4]);
-                nib_pairs(w.z, &pa[t][r][8]);
-                nib_pairs(w.w, &pa[t][r][12]);
-                const int g = r * (H / 64) + (lane >> 1);
-                ks_a[t][r] = bf16_to_f32(reinterpret_cast<const uint16_t*>(SA_.s[t])[g]);
-                kc_a[t][r] = affine_c(ks_a[t][r], reinterpret_cast<const uint16_t*>(SA_.b[t])[g]);
-            }
+        for (int r = 0; r < RA; ++r) {
+            const uint4 w = SA_.w[t][r][lane];
+            nib_pairs(w.x, &pa[t][r][0]);
+            nib_pairs(w.y, &pa[t][r][4]);
+            nib_pairs(w.z, &pa[t][r][8]);
+            nib_pairs(w.w, &pa[t][r][12]);
+            const int g = r * (H / 64) + (lane >> 1);
+            ks_a[t][r] = bf16_to_f32(reinterpret_cast<const uint16_t*>(SA_.s[t])[g]);
+            kc_a[t][r] = affine_c(ks_a[t][r], reinterpret_cast<const uint16_t*>(SA_.b[t])[g]);
+        }
         // done now, while the exchange runs, not after the next barrier
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int r = 0; r < RA; ++r) {
 #pragma unroll
-            for (int r = 0; r < RA; ++r) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) pin(pa[t][r][i]);
-                pin(ks_a[t][r]);
-                pin(kc_a[t][r]);
-            }
+            for (int i = 0; i < 16; ++i) pin(pa[t][r][i]);
+            pin(ks_a[t][r]);
+            pin(kc_a[t][r]);
+        }
     };
     uint32_t pb[SPL_B][16];
     float ks_b[SPL_B], kc_b[SPL_B];
@@ -523,12 +570,22 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         }
     };
 
-    // One layer; false if the step was aborted.  On entry this layer's up
-    // weights are staged and its gate weights (this wave's own DMA) issued;
-    // its down weights are staged by B3.
-    auto layer = [&](int l) -> bool {
-        wait_vmcnt<0>();                                       // own gate-row DMA
-        unpackA();                                             // while x is gathered
+    // One layer; false if the step was aborted.  On entry this layer's gate
+    // weights (this wave's own DMA) are issued and its up weights staged
+    // (layer 0: issued by this wave too); its down weights are staged by B3.
+    // (inlined twice: layer 0 is peeled, so that its copy waits for the
+    // prologue's untracked DMA by exact counts, gate rows first)
+    auto layer = [&](int l) __attribute__((always_inline)) -> bool {
+        if (l == 0) {                                          // own gate and up DMA of the prologue
+            wait_vmcnt<kDmaA / 2>();                           // gate rows (up rows still landing)
+            unpackA(0);
+            wait_vmcnt<0>();
+            unpackA(1);
+        } else {
+            wait_vmcnt<0>();                                   // own gate-row DMA
+            unpackA(0);                                        // while x is gathered
+            unpackA(1);
+        }
         lds_barrier();                                         // B1
         if (sm.abort) return false;
         if (l + 1 < L) dmaA(cw, l + 1, 0);                     // during the RMSNorm phase
@@ -593,10 +650,9 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
         return true;
     };
 
-    lds_barrier();                                             // B0
-    bool aborted = false;
-    for (int l = 0; l < L; ++l)
-        if (!layer(l)) { aborted = true; break; }
+    bool aborted = L > 0 && !layer(0);
+    for (int l = 1; l < L && !aborted; ++l)
+        if (!layer(l)) aborted = true;
 
     // ---- lm_head + argmax over this wave's batches ----
     // (first two batches issued here, once the layer weights are dead, so they
