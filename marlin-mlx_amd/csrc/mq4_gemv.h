@@ -62,8 +62,8 @@ void launch_combine2_residual(const float* part, int M, int N, const uint16_t* r
 
 // The lm_head + argmax (EPI_ARGMAX, K = 2048, 1 <= m_valid <= kMfmaMaxM)
 // with a ring of weight tiles in flight per CU (mq4_lmring.hip): for 1-2
-// rows the dot2 GEMV's arithmetic (N a multiple of 4), from 3 rows the MFMA
-// GEMV's, each bit-identical to that kernel's logits and tokens.  Enqueues it and the
+// rows the dot2 GEMV's arithmetic, from 3 rows the MFMA GEMV's, each
+// bit-identical to that kernel's logits and tokens.  Enqueues it and the
 // argmax finalize and returns 0, or -1 for shapes and alignments it does not
 // take (x, wq and the norm weight 16-byte, scales and biases 4-byte aligned).
 int launch_lm_ring(const GemvParams& a, bool norm, hipStream_t st);

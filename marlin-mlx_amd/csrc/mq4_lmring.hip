@@ -79,8 +79,21 @@ __global__ __launch_bounds__(kThreads) void lm_ring_kernel(Params p) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c16 = lane & 15, kq = lane >> 4;
     const int M = p.M, N = p.N, g0 = wave * GWA;
-    const int ntiles = (N + 15) / 16;
-    const int T = (int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    // Rows in R full rounds of 16-row tiles (tile j of workgroup b: rows
+    // 16 (b + j G) ..), and the remaining rem < 16 G rows as one short tile
+    // of at most q = ceil(rem / G) rows per workgroup, taken first: its
+    // round trip then overlaps the ring's start instead of adding a last
+    // round on a fraction of the CUs.  A short tile's missing rows repeat
+    // its last row and are not reported.
+    const int G = (int)gridDim.x, bx = (int)blockIdx.x;
+    const int R = N / (16 * G), rem = N - R * 16 * G;
+    const int q = (rem + G - 1) / G;
+    const int rshort = R * 16 * G + bx * q;
+    const int nshort = rem == 0 ? 0 : (N - rshort < q ? (N - rshort > 0 ? N - rshort : 0) : q);
+    const int S = nshort > 0 ? 1 : 0;
+    const int T = R + S;
+    auto tile_n0 = [&](int j) { return j < S ? rshort : 16 * (bx + (j - S) * G); };
+    auto tile_rows = [&](int j) { return j < S ? nshort : 16; };
 
     // ---- activations and norm weights (tracked loads, waited for before any DMA) ----
     uint4 xa[MT][GWA][2];
@@ -122,14 +135,14 @@ __global__ __launch_bounds__(kThreads) void lm_ring_kernel(Params p) {
 
     // ---- the ring: tile j of this workgroup -> slot j % kR ----
     auto issue = [&](int j, int slot) {
-        const int n0 = 16 * ((int)blockIdx.x + j * (int)gridDim.x);
+        const int n0 = tile_n0(j), nl = n0 + tile_rows(j) - 1;  // rows past nl repeat row nl, never used
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int sl = 64 * b + lane, row = sl >> 3, u = stage_chunk(sl, row);
-            const int n = n0 + row < N ? n0 + row : N - 1;     // rows past N repeat row N - 1, never used
+            const int n = n0 + row < nl ? n0 + row : nl;
             dma16(p.A.wq + (int64_t)n * (K / 8) + 32 * wave + 4 * u, &sm.w[wave][slot][b][0]);
         }
-        const int r = (lane & 31) >> 1, n = n0 + r < N ? n0 + r : N - 1;
+        const int r = (lane & 31) >> 1, n = n0 + r < nl ? n0 + r : nl;
         const uint16_t* src = lane < 32 ? p.A.s : p.A.b;
         dma4(src + (int64_t)n * GA + GWA * wave + 2 * (lane & 1), &sm.sb[wave][slot][0]);
     };
@@ -209,8 +222,8 @@ __global__ __launch_bounds__(kThreads) void lm_ring_kernel(Params p) {
             float v = rp[0];
 #pragma unroll
             for (int w = 1; w < kWaves; ++w) v += rp[w * kStride];
-            const int n = 16 * ((int)blockIdx.x + j * (int)gridDim.x) + r_c;
-            if (r_m < M && n < N) {
+            const int n = tile_n0(j) + r_c;
+            if (r_m < M && r_c < tile_rows(j)) {
                 const uint32_t lb = f32_to_bf16(v);
                 if (p.y) p.y[(int64_t)r_m * N + n] = (uint16_t)lb;
                 const uint64_t key = argmax_key(lb, (uint32_t)n);
@@ -275,21 +288,42 @@ __global__ __launch_bounds__(kThreads) void lm_ring_dot2_kernel(lmr::Params p) {
     __shared__ Smem sm;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int N = p.N;                                 // a multiple of RPI (checked by the host)
-    const int nb = N / RPI;
+    // Rows in R full rounds of RPI-row batches (batch j of wave gw: rows
+    // RPI (gw + j W) ..), then the remaining rem < RPI W rows as one short
+    // batch of at most q = ceil(rem / W) rows per wave, dealt wave-major
+    // (wave v of every workgroup before wave v + 1 of any), so that every
+    // CU ends within a few rows of the others: a last round of whole batches
+    // on a fraction of the CUs cost 1.2-1.6 us at N = 248320.  A short
+    // batch's missing rows get a 256-byte DMA of its last row instead (the
+    // same DMA count per batch, a quarter of the bytes) and are not reported.
+    const int N = p.N;
     const int gw = (int)blockIdx.x * kWaves + wave, W = (int)gridDim.x * kWaves;
-    const int T = gw < nb ? (nb - 1 - gw) / W + 1 : 0;
+    const int R = N / (RPI * W), rem = N - R * RPI * W;
+    const int q = (rem + W - 1) / W;
+    const int rlast = R * RPI * W + (wave * (int)gridDim.x + (int)blockIdx.x) * q;   // short batch
+    const int nlast = rem == 0 ? 0 : (N - rlast < q ? (N - rlast > 0 ? N - rlast : 0) : q);
+    const int S = nlast > 0 ? 1 : 0;                           // the short batch goes first
+    const int T = R + S;
+    auto first_row = [&](int j) { return j < S ? rlast : RPI * (gw + (j - S) * W); };
+    auto batch_rows = [&](int j) { return j < S ? nlast : RPI; };
     const char* wq = reinterpret_cast<const char*>(p.A.wq);
     const char* sq = reinterpret_cast<const char*>(p.A.s);
     const char* bq = reinterpret_cast<const char*>(p.A.b);
 
     auto issue = [&](int j, int slot) {
-        const int64_t r0 = (int64_t)RPI * (gw + j * W);
+        const int64_t r0 = first_row(j);
+        const int nr = batch_rows(j);
 #pragma unroll
-        for (int r = 0; r < RPI; ++r)
-            stage::dma16_s(wq + (r0 + r) * (K / 2), 16u * lane, &sm.w[wave][slot][r][0]);
-        stage::dma4_s(sq + r0 * (K / 32), 4u * lane, &sm.sb[wave][slot][0][0]);
-        stage::dma4_s(bq + r0 * (K / 32), 4u * lane, &sm.sb[wave][slot][1][0]);
+        for (int r = 0; r < RPI; ++r) {
+            if (r < nr)
+                stage::dma16_s(wq + (r0 + r) * (K / 2), 16u * lane, &sm.w[wave][slot][r][0]);
+            else
+                stage::dma4_s(wq + (r0 + nr - 1) * (K / 2), 4u * lane, &sm.w[wave][slot][r][0]);
+        }
+        // scales and biases: lane l holds dword l % 16 of row l / 16
+        const uint32_t sbo = 64u * (uint32_t)((lane >> 4) < nr ? (lane >> 4) : nr - 1) + 4u * (lane & 15);
+        stage::dma4_s(sq + r0 * (K / 32), sbo, &sm.sb[wave][slot][0][0]);
+        stage::dma4_s(bq + r0 * (K / 32), sbo, &sm.sb[wave][slot][1][0]);
     };
 #pragma unroll
     for (int j = 0; j < kRD; ++j)
@@ -376,8 +410,8 @@ __global__ __launch_bounds__(kThreads) void lm_ring_dot2_kernel(lmr::Params p) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (j + kRD < T) issue(j + kRD, slot);
         const float val = wave_multi_reduce<V>(acc, lane);
-        const int vidx = lane >> SH, m = vidx % M, row = RPI * (gw + j * W) + vidx / M;
-        if ((lane & ((1 << SH) - 1)) == 0 && m < p.M) {
+        const int vidx = lane >> SH, m = vidx % M, row = first_row(j) + vidx / M;
+        if ((lane & ((1 << SH) - 1)) == 0 && m < p.M && vidx / M < batch_rows(j)) {
             const uint32_t lb = f32_to_bf16(val);
             if (p.y) p.y[(int64_t)m * N + row] = (uint16_t)lb;
             const uint64_t key = argmax_key(lb, (uint32_t)row);
@@ -406,7 +440,6 @@ __global__ __launch_bounds__(kThreads) void lm_ring_dot2_kernel(lmr::Params p) {
 
 int launch_lm_ring(const GemvParams& a, bool norm, hipStream_t st) {
     if (a.K != lmr::K || a.m_valid < 1 || a.m_valid > lmr::kMaxM || a.N < 1 || !a.partial || !a.idx) return -1;
-    if (a.m_valid <= 2 && a.N % lmd::RPI != 0) return -1;   // the 1-2 row kernel reads whole 4-row batches
     if (!aligned(a.x, 16) || !aligned(a.A.wq, 16) || !aligned(a.A.s, 4) || !aligned(a.A.b, 4)) return -1;
     if (norm && !aligned(a.norm_w, 16)) return -1;
     const int ntiles = (a.N + 15) / 16;

@@ -187,8 +187,8 @@ def test_batched_edge_shapes(mq4, O, dev, case):
         check_close(O, lg, y64, f"edge {case}")
 
 
-@pytest.mark.parametrize("M,N", [(1, V), (2, V), (1, 17), (2, 4097), (5, V), (16, V), (17, V), (32, V),
-                                 (16, 1000), (20, 4097), (8, 17)])
+@pytest.mark.parametrize("M,N", [(1, V), (2, V), (1, 17), (2, 4097), (1, 4097), (1, 26384), (2, 21383),
+                                 (5, V), (16, V), (17, V), (32, V), (16, 1000), (20, 4097), (8, 17)])
 def test_lm_head_ring_equals_mfma_gemv(mq4, O, dev, lm, M, N):
     """From 5 rows at K = 2048 the lm_head + argmax runs as the weight-ring
     kernel (mq4_lmring.hip): the MFMA GEMV's arithmetic (8 waves x 4 groups,
@@ -197,7 +197,10 @@ def test_lm_head_ring_equals_mfma_gemv(mq4, O, dev, lm, M, N):
     the dot2 GEMV, whose plain product is the same kernel with another
     epilogue.  The tokens are the argmax of those logits.  Ragged N: fewer
     tiles than workgroups (1000 and 17 rows) and a last tile of one row
-    (4097)."""
+    (4097); for 1-2 rows, whose rows past the full rounds of 4-row batches
+    go out as short batches of up to ceil(rest / waves) rows, rests of one
+    row per wave (248320), two (4097, 21383: the last wave's batch cut to
+    one row) and three (26384)."""
     print(f"lm_head ring vs MFMA GEMV: M={M} N={N}", flush=True)
     qt = lm[0] if N == V else mq4.quantize_weight(
         mq4.fill_normal_bf16((N, H), 7100 + N, 0.0, 0.02, device=dev))
