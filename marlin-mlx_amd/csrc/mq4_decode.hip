@@ -550,20 +550,33 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
 
     // lm_head streaming state: this wave's batches of LM_RPI rows, LM_NBUF
     // register buffers so that LM_NBUF - 1 batches are in flight while one is
-    // reduced
+    // reduced.  Rows: lm_full full rounds of LM_RPI-row batches (batch j of
+    // wave gw: rows LM_RPI (gw + j W)), and the rest (fewer than a round) as
+    // one short batch of at most ceil(rest / W) rows per wave, dealt
+    // wave-major and taken first, so that its round trip overlaps the start
+    // of the stream instead of adding a last round (a 31st round of whole
+    // batches at vocab 248,320); its missing rows repeat its last row and
+    // are not reported.
+    constexpr int W = kNWG * kNCW;
     const int gw = wg * kNCW + cw;
-    const int n_lm_batches = (p.vocab + LM_RPI - 1) / LM_RPI;
-    const int lm_rounds = (n_lm_batches + kNWG * kNCW - 1) / (kNWG * kNCW);
+    const int lm_full = p.vocab / (LM_RPI * W), lm_rest = p.vocab - lm_full * LM_RPI * W;
+    const int lm_q = (lm_rest + W - 1) / W;
+    const int lm_r0s = lm_full * LM_RPI * W + (cw * kNWG + wg) * lm_q;     // short batch
+    const int lm_ns = lm_rest == 0 ? 0 : (p.vocab - lm_r0s < lm_q ? (p.vocab - lm_r0s > 0 ? p.vocab - lm_r0s : 0) : lm_q);
+    const int lm_S = lm_ns > 0 ? 1 : 0;
+    const int lm_rounds = lm_full + lm_S;
+    auto lm_row0 = [&](int j) { return j < lm_S ? lm_r0s : LM_RPI * (gw + (j - lm_S) * W); };
+    auto lm_nrows = [&](int j) { return j < lm_S ? lm_ns : LM_RPI; };
     struct LmBuf {
         uint4 w[LM_RPI];
         uint32_t s[LM_RPI], b[LM_RPI];
     };
     LmBuf lb[LM_NBUF];
     auto loadLM = [&](LmBuf& B, int round) {
-        const int r0 = (round * kNWG * kNCW + gw) * LM_RPI;
+        const int r0 = lm_row0(round), rl = r0 + lm_nrows(round) - 1;
 #pragma unroll
         for (int r = 0; r < LM_RPI; ++r) {
-            const int row = (r0 + r) < p.vocab ? (r0 + r) : (p.vocab - 1);
+            const int row = r0 + r < rl ? r0 + r : rl;
             B.w[r] = load_nt_u4(reinterpret_cast<const uint4*>(p.lm.wq + (int64_t)row * (H / 8)) + lane);
             B.s[r] = p.lm.s[(int64_t)row * (H / 64) + (lane >> 1)];
             B.b[r] = p.lm.b[(int64_t)row * (H / 64) + (lane >> 1)];
@@ -684,8 +697,8 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(Params p) {
             if (round + LM_NBUF < lm_rounds) loadLM(B, round + LM_NBUF);   // refill LM_NBUF rounds ahead
             const float v = wave_multi_reduce<LM_RPI>(acc, lane);
             constexpr int SHL = 6 - log2_const<LM_RPI>();
-            const int row = (round * kNWG * kNCW + gw) * LM_RPI + (lane >> SHL);
-            if ((lane & ((1 << SHL) - 1)) == 0 && row < p.vocab) {
+            const int row = lm_row0(round) + (lane >> SHL);
+            if ((lane & ((1 << SHL) - 1)) == 0 && (lane >> SHL) < lm_nrows(round)) {
                 const uint64_t key = argmax_key(f32_to_bf16(v), (uint32_t)row);
                 best = key > best ? key : best;
             }
