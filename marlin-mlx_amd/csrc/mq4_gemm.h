@@ -38,6 +38,32 @@ struct GemmArgs {
 // (a.xsum set: no fused norm, K/64 even, scale/bias rows 4-byte aligned).
 int launch_q4_gemm(const GemmArgs& a, int epi, bool norm, hipStream_t st);
 
+// The fp16-weight GEMM (mq4_gemm16.hip): x holds fp16 activations in the
+// operand order of launch_pair_rows16, row m scaled by 1 / xscale[m] (null:
+// 1), and the product of row m is multiplied by xscale[m].  Epilogues as
+// GemmArgs (GEMM_SWIGLU with ysum: N % 128 == 0).
+struct Gemm16Args {
+    const uint16_t* x;       // [M, K] fp16, operand order
+    const float* xscale;     // [M] powers of two, or null
+    int M, N, K;
+    QMat A, B;
+    void* y;
+    const uint16_t* res;
+    float* ysum;
+};
+
+// Enqueue the fp16-weight GEMM; 0, or -1 for shapes it does not take (K % 512
+// != 0, scales or biases not 16-byte aligned, byte offsets past 32 bits).
+int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st);
+
+// xp = fp16(x / xscale[m]) (norm_w null) or fp16(bf16(x * rsqrt(mean(x^2) +
+// eps) * (1 + norm_w)) / xscale[m]) in the operand order (the bits of
+// mq4_rms_norm before the conversion), with xscale[m] = 2^e, e >= 0 the
+// smallest that keeps the row below 2^15.  K % 512 == 0; x, xp, norm_w
+// 16-byte aligned.
+int launch_pair_rows16(const uint16_t* x, int M, int K, const uint16_t* norm_w, float eps, uint16_t* xp,
+                       float* xscale, hipStream_t st);
+
 // xp = x (norm_w null) or bf16(x * rsqrt(mean(x^2) + eps) * (1 + norm_w)),
 // the bits of mq4_rms_norm, with every 8-element chunk of a row in the
 // pair order above, and xs[g * M + m] = the fp32 sum of group g of row m

@@ -1,0 +1,485 @@
+// Prefill-shaped (large M) MLX-affine Q4 GEMM for gfx950 with the weights
+// dequantized to fp16 in registers and fed to the fp16 MFMA.
+//
+// Same call sites as mq4_gemm.hip: qmatmul (src/model/marlin.cpp:18-25)
+// inside mlp_forward (:31-35) over all S prompt tokens, with the rms_norm in
+// front (:141, :12-16) and the swiglu (:27-29) fused in; used for the gate/up
+// product of mq4_mlp_residual.
+//
+//   Y[M, N] = X[M, K] . W[N, K]^T,  W[n, k] = s[n, g] * q[n, k] + b[n, g],  g = k / 64
+//
+// mq4_gemm.hip keeps both MFMA operands exact (x and 128 + q in bf16) and
+// folds every group into the fp32 result with the VALU, two instructions per
+// output and group: at 64 x 64 outputs per wave that fold is as long as the
+// group's MFMAs, and the kernel is VALU-bound.  Here each weight is formed
+// once as w = fp16(s q + b), one rounding (v_pk_fma_f16 on exact fp16 q, s
+// and b), and the MFMA accumulates x . w straight into the result: no fold.
+// s q + b of a bf16 scale and bias and a 4-bit q mostly fits fp16's 11-bit
+// significand, so most weights are exact; on 0.02-std Gaussian weights the
+// product's error is 2.4e-6 of the output rms (max 1.5e-4), against about
+// 1e-5 for the exact-operand kernel's fp32 fold.  Scales and biases convert
+// to fp16 exactly in its normal range (beyond 65504 a weight would not be
+// finite; below 2^-14 the conversion is subnormal, an absolute error under
+// 2^-25).
+//
+// The activations are an fp16 copy of the bf16 operand in the MFMA pair
+// order (launch_pair_rows16: normalized x), each row scaled by a power of two
+// 2^-e (e = 0 unless the row holds values of 2^15 or more) that the epilogue
+// multiplies back exactly, so any bf16 input stays finite.  A bf16 value
+// converts to fp16 exactly unless it lies below 2^-14 (2^-14 + e), where
+// fp16 is subnormal: an absolute error under 2^-25 of the row's scale.
+//
+// Work decomposition:
+//  * A 256-thread block computes 128 rows x 256 weight columns (one matrix:
+//    256 output columns; gate and up: 128 output columns each, for the fused
+//    SwiGLU); wave w takes all 128 rows and 64 weight columns (gate/up:
+//    32 gate and the same 32 up columns) as 4 x 2 v_mfma_f32_32x32x16_f16
+//    tiles, so each weight is dequantized once per block, by the one wave
+//    that uses it (about two VALU per weight: a v_and_or_b32 forms two fp16
+//    1024 + q, a v_pk_add_f16 takes the 1024 off, a v_pk_fma_f16 applies s
+//    and b to the pair).
+//  * Per 64-k group, the 128 x 64 activations (16 KB, each row's eight
+//    16-byte chunks XOR-swizzled by (row / 2) % 8: the 16 lanes of a
+//    ds_read_b128 phase, 16 rows at one chunk, cover the 64 banks once) and
+//    the 256 x 32 bytes of packed weights (two lanes per weight column, its
+//    32 contiguous bytes) go to LDS by DMA, two stages, one group ahead;
+//    the columns' scales and biases follow every eight groups (16 bytes per
+//    column, two slots).  Each step waits for all of its wave's DMA;
+//    barriers carry no memory fence.  (Per-group DMA of the scales, four
+//    bytes from 64 columns per instruction, and of one k-half of 64 columns
+//    made the kernel bound by L2 requests: 17.5 M per gate/up call at M =
+//    2048.)
+//  * The operand layout is mq4_gemm.hip's: lane l of a tile holds row (or
+//    weight column) l % 32 and k-half l / 32; MFMA step ks takes word ks of
+//    the half, whose nibble pairs (q_p, q_{p+4}) meet the activations in the
+//    pair order (x_p, x_{p+4}) of the pre-pass.
+#include <type_traits>
+
+#include "mq4_device.h"
+#include "mq4_gemm.h"
+#include "mq4_host.h"
+
+namespace mq4 {
+
+namespace g16 {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kNW = 4;                    // waves per block
+constexpr int kThreads = 64 * kNW;
+constexpr int TBM = 128;                  // rows per block
+constexpr int BNW = 64 * kNW;             // weight columns per block
+constexpr int A_I = TBM * 8 / (64 * kNW); // activation DMA instructions per wave and group (4)
+constexpr int B_TOT = 2 * BNW / 64;       // weight DMA instructions per block and group (8)
+constexpr int B_I = B_TOT / kNW;          // per wave (2)
+constexpr int SB_I = 2 * BNW / (64 * kNW);// scale/bias DMA instructions per wave and 8 groups (2)
+
+struct Stage {
+    uint4 a[TBM * 8];                     // [row][chunk ^ ((row >> 1) & 7)], fp16 pairs
+    uint4 b[2 * BNW];                     // [weight column][k-half]
+};
+// Scales and biases of 8 groups: [scales | biases][weight column], 16 bytes
+// (groups 8 t .. 8 t + 7) each.
+struct SbStage {
+    uint4 v[2][BNW];
+};
+static_assert(2 * sizeof(Stage) + 2 * sizeof(SbStage) <= 65536, "LDS DMA targets must lie in the first 64 KiB");
+
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+}
+
+// bf16 bits -> fp16 (round to nearest even; exact for bf16 values of fp16's
+// normal range)
+__device__ __forceinline__ _Float16 bf16_to_h(uint32_t bits) { return (_Float16)bf16_to_f32(bits); }
+
+// fp16 (1024 + q_p, 1024 + q_{p+4}) of nibbles p, p + 4 of s: one
+// v_and_or_b32 with the mask in an SGPR and the exponent bits in a VGPR,
+// both set up once by the caller.
+__device__ __forceinline__ uint32_t nib_pair_h(uint32_t s, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(s), "s"(m), "v"(c));
+    return r;
+}
+
+// The eight fp16 weights fp16(s q + b) of one packed word, in the nibble-pair
+// order (q0, q4), (q1, q5), (q2, q6), (q3, q7).
+__device__ __forceinline__ h8_t dequant_word(uint32_t w, h2_t s2, h2_t b2, uint32_t m, uint32_t c) {
+    const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    uint32_t out[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const h2_t q = __builtin_bit_cast(h2_t, nib_pair_h(w >> (4 * p), m, c)) - k1024;   // exact
+        out[p] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
+    }
+    return __builtin_bit_cast(h8_t, make_uint4(out[0], out[1], out[2], out[3]));
+}
+
+// MFMA results are read by the VALU only in the epilogue; the padding keeps
+// the wait states between the last MFMA and that read generous.
+__device__ __forceinline__ void mfma_result_pad() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
+#pragma clang fp contract(off)
+    constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
+    constexpr int BN = BNW / NMAT;                       // output columns per block
+    __shared__ Stage st0, st1;
+    __shared__ SbStage sb0, sb1;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, col = lane & 31;
+    const int M = p.M, N = p.N, K = p.K, G = K / 64;
+
+    // XCD-aware block order: with the column blocks a multiple of 8, XCD x
+    // (block b runs on XCD b % 8) takes a fixed eighth of them for every row
+    // block, so its weights stay in its own L2
+    const int NB = (N + BN - 1) / BN;
+    int nb, mb;
+    {
+        const int b = blockIdx.x;
+        if ((NB & 7) == 0) {
+            const int per = NB >> 3, s = b >> 3;
+            nb = (s % per) * 8 + (b & 7);
+            mb = s / per;
+        } else {
+            nb = b % NB;
+            mb = b / NB;
+        }
+    }
+    const int n0 = nb * BN, m0 = mb * TBM;
+
+    // ---- DMA sources: wave-uniform bases plus 32-bit lane byte offsets ----
+    const char* const xbase = reinterpret_cast<const char*>(p.x);
+    uint32_t aoff[A_I];
+#pragma unroll
+    for (int t = 0; t < A_I; ++t) {
+        const int slot = (wave * A_I + t) * 64 + lane;
+        const int r = slot >> 3, c = (slot & 7) ^ ((r >> 1) & 7);
+        const int row = (m0 + r) < M ? (m0 + r) : (M - 1);
+        aoff[t] = (uint32_t)(((int64_t)row * K + c * 8) * 2);
+    }
+    // weight column r of the block -> matrix and output row (rows past N
+    // repeat row N - 1, never stored)
+    auto wrow_of = [&](int r) -> int {
+        const int n = NMAT == 2 ? n0 + (r % (BNW / 2)) : n0 + r;
+        return n < N ? n : N - 1;
+    };
+    auto mat_of = [&](int r) -> const QMat& { return (NMAT == 2 && r >= BNW / 2) ? p.B : p.A; };
+    // packed weights: instruction t covers 32 weight columns, two lanes per
+    // column (its group's two 16-byte k-halves, 32 contiguous bytes)
+    const char* bbase[B_I];
+    uint32_t boff[B_I];
+#pragma unroll
+    for (int t = 0; t < B_I; ++t) {
+        const int q0 = (wave * B_I + t) * 64, r0 = q0 >> 1;
+        bbase[t] = reinterpret_cast<const char*>(mat_of(r0).wq);
+        boff[t] = (uint32_t)((int64_t)wrow_of(r0 + (lane >> 1)) * (K / 2) + (lane & 1) * 16);
+    }
+    // scales and biases: 16 bytes (8 groups) of one weight column per lane
+    const char* sbbase[SB_I];
+    uint32_t sboff[SB_I];
+#pragma unroll
+    for (int t = 0; t < SB_I; ++t) {
+        const int u0 = (wave * SB_I + t) * 64, sel = u0 / BNW, r0 = u0 % BNW;
+        sbbase[t] = reinterpret_cast<const char*>(sel ? mat_of(r0).b : mat_of(r0).s);
+        sboff[t] = (uint32_t)((int64_t)wrow_of(r0 + lane) * G * 2);
+    }
+    auto issue = [&](int g, Stage& st) {
+#pragma unroll
+        for (int t = 0; t < A_I; ++t) lds_dma16(xbase + g * 128 + aoff[t], &st.a[(wave * A_I + t) * 64]);
+#pragma unroll
+        for (int t = 0; t < B_I; ++t) lds_dma16(bbase[t] + g * 32 + boff[t], &st.b[(wave * B_I + t) * 64]);
+    };
+    auto issue_sb = [&](int t8, SbStage& sbs) {        // groups 8 t8 .. 8 t8 + 7
+#pragma unroll
+        for (int t = 0; t < SB_I; ++t) lds_dma16(sbbase[t] + t8 * 16 + sboff[t], &sbs.v[0][(wave * SB_I + t) * 64]);
+    };
+
+    // ---- this lane's weight columns (block-relative) of tiles j = 0, 1 ----
+    int wr[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wave * 32 + col : wave * 64 + j * 32 + col;
+
+    uint32_t nib_mask, nib_exp;               // the nibble-pair constants, set up once
+    asm("s_mov_b32 %0, 0x000f000f" : "=s"(nib_mask));
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(nib_exp));
+
+    f32x16_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // this group's packed words, scales and biases (read before the step's
+    // DMA is issued, so no wait for it can come between)
+    struct Wts {
+        uint4 bw[2];
+        h2_t s2[2], b2[2];
+    };
+    auto load_wts = [&](int g, const Stage& st) -> Wts {
+        Wts w;
+        const SbStage& sbs = ((g >> 3) & 1) ? sb1 : sb0;
+        const int sh16 = (g & 1) * 16, dw = (g >> 1) & 3;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            w.bw[j] = st.b[wr[j] * 2 + h];
+            const _Float16 s = bf16_to_h((reinterpret_cast<const uint32_t*>(&sbs.v[0][wr[j]])[dw] >> sh16) & 0xffffu);
+            const _Float16 b = bf16_to_h((reinterpret_cast<const uint32_t*>(&sbs.v[1][wr[j]])[dw] >> sh16) & 0xffffu);
+            w.s2[j] = (h2_t){s, s};
+            w.b2[j] = (h2_t){b, b};
+        }
+        return w;
+    };
+    auto compute = [&](const Wts& wt, const Stage& st) {
+        const uint4* bw = wt.bw;
+        const h2_t* s2 = wt.s2;
+        const h2_t* b2 = wt.b2;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            h8_t a[4], bo[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = i * 32 + col, ch = 4 * h + ks;
+                a[i] = __builtin_bit_cast(h8_t, st.a[r * 8 + (ch ^ ((r >> 1) & 7))]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t w = ks == 0 ? bw[j].x : ks == 1 ? bw[j].y : ks == 2 ? bw[j].z : bw[j].w;
+                bo[j] = dequant_word(w, s2[j], b2[j], nib_mask, nib_exp);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bo[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    // Two stages: step g waits for all of this wave's DMA (group g's), meets
+    // the other waves at the barrier, reads group g's weights, issues group
+    // g + 1 into the stage read in step g - 1 (past the end: the last group
+    // again, into a stage nobody reads), at every eighth group also the next
+    // eight groups' scales and biases into the slot read by the eight groups
+    // before, and computes group g.
+    auto step = [&](int g, const Stage& cur, Stage& nxt) {
+        wait_vmcnt<0>();
+        lds_barrier();                               // group g is in `cur` for every wave
+        const Wts wt = load_wts(g, cur);
+        issue(g + 1 < G ? g + 1 : G - 1, nxt);       // into the stage read in step g - 1
+        if ((g & 7) == 0 && g + 8 < G) issue_sb((g >> 3) + 1, ((g >> 3) & 1) ? sb0 : sb1);
+        compute(wt, cur);
+    };
+    issue(0, st0);
+    issue_sb(0, sb0);
+    int g0 = 0;
+    for (; g0 + 2 <= G; g0 += 2) {
+        step(g0, st0, st1);
+        step(g0 + 1, st1, st0);
+    }
+    if (g0 < G) step(g0, st0, st1);
+    wait_vmcnt<0>();                                 // no DMA outstanding past the loop
+    mfma_result_pad();
+
+    // ---- epilogue: lane l of a 32 x 32 tile holds rows (e/4)*8 + (l/32)*4 + e%4, column l%32 ----
+    // SwiGLU with ysum: h goes out in the operand order (column c of a chunk
+    // at 2 (c % 4) + c / 4) and the group sums of its rows through LDS, 64
+    // rows at a time (stage 0, free once every wave is past its last group)
+    const bool paired_out = EPI == GEMM_SWIGLU && p.ysum != nullptr;
+    constexpr int TS = BN + 8;                                     // bf16 per epilogue tile row
+    uint16_t* tile = reinterpret_cast<uint16_t*>(&st0);          // [64][TS] bf16
+    static_assert(64 * (BNW / 2 + 8) * 2 <= (int)sizeof(Stage), "epilogue tile");
+    auto emit = [&](int i, int rbase) {
+        float sc[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
+            sc[e] = p.xscale && row < M ? p.xscale[row] : 1.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
+            const int cn = NMAT == 2 ? n0 + wave * 32 + col : n0 + wave * 64 + j * 32 + col;
+            const int cw = paired_out ? ((cn & ~7) | (2 * (cn & 3) + ((cn >> 2) & 1))) : cn;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int rl = i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
+                const int row = m0 + rl;
+                if (EPI == GEMM_SWIGLU) {
+                    const uint32_t v = swiglu_bf16(acc[i][0][e] * sc[e], acc[i][1][e] * sc[e]);
+                    if (paired_out) tile[(rl - rbase) * TS + wave * 32 + col] = (uint16_t)v;
+                    if (row < M && cn < N) reinterpret_cast<uint16_t*>(p.y)[(int64_t)row * N + cw] = (uint16_t)v;
+                    continue;
+                }
+                if (row >= M || cn >= N) continue;
+                const int64_t o = (int64_t)row * N + cn;
+                const float v = acc[i][j][e] * sc[e];
+                if (EPI == GEMM_STORE) {
+                    reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)f32_to_bf16(v);
+                } else if (EPI == GEMM_STORE_F32) {
+                    reinterpret_cast<float*>(p.y)[o] = v;
+                } else {
+                    reinterpret_cast<uint16_t*>(p.y)[o] =
+                        (uint16_t)f32_to_bf16(bf16_to_f32(p.res[o]) + round_bf16(v));
+                }
+            }
+        }
+    };
+    // ysum of group n0 / 64 + gi of rows rbase .. rbase + 63: thread t takes
+    // row t / 4, group (t / 2) % 2 and half t % 2 (32 values summed left to
+    // right), then the two halves are added (the order of mq4_gemm.hip's
+    // paired SwiGLU output)
+    auto group_sums = [&](int rbase) {
+        const int rl = tid >> 2, gi = (tid >> 1) & 1, hf = tid & 1;
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 v = *reinterpret_cast<const uint4*>(&tile[rl * TS + gi * 64 + hf * 32 + c * 8]);
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sum += bf16_to_f32(w4[q] & 0xffffu);
+                sum += bf16_to_f32(w4[q] >> 16);
+            }
+        }
+        const float other = __shfl_xor(sum, 1);
+        if (hf == 0 && m0 + rbase + rl < M)
+            p.ysum[(int64_t)((n0 >> 6) + gi) * M + m0 + rbase + rl] = sum + other;
+    };
+    if (paired_out) {
+        static_assert(kThreads == 4 * 64, "four threads per tile row");
+        __syncthreads();                                           // every wave is done with the stages
+        emit(0, 0);
+        emit(1, 0);
+        __syncthreads();
+        group_sums(0);
+        __syncthreads();                                           // the tile is read before rows 64-127
+        emit(2, 64);
+        emit(3, 64);
+        __syncthreads();
+        group_sums(64);
+    } else {
+        emit(0, 0);
+        emit(1, 0);
+        emit(2, 0);
+        emit(3, 0);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Activation pre-pass: one wave per row.  Pass 1 forms the row's sum of
+// squares (with the norm; the per-element formula of mq4_rms_norm) and the
+// largest |x (1 + w)| (|x| without the norm); pass 2 writes bf16(x r (1 + w))
+// (or x), scaled by 2^-e and converted to fp16, in the pair order, and
+// xscale[m] = 2^e.  e is the smallest such that the scaled row stays below
+// 2^15 (0 for every normalized row whose values stay below 2^15).
+template <bool NORM>
+__global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                          const uint16_t* __restrict__ nw, float eps,
+                                                          uint16_t* __restrict__ xp, float* __restrict__ xscale) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;                                  // whole waves
+    const int CH = K / 8;
+    const uint4* src = reinterpret_cast<const uint4*>(x + (int64_t)m * K);
+    uint4* dst = reinterpret_cast<uint4*>(xp + (int64_t)m * K);
+    float ss = 0.0f, big = 0.0f;
+    for (int c = lane; c < CH; c += 64) {
+        const uint4 v = src[c];
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+        uint4 wv = make_uint4(0, 0, 0, 0);
+        if (NORM) wv = reinterpret_cast<const uint4*>(nw)[c];
+        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (NORM) ss = sumsq_word(ss, vw[q]);
+            const float a0 = bf16_to_f32(vw[q] & 0xffffu), a1 = bf16_to_f32(vw[q] >> 16);
+            const float f0 = NORM ? 1.0f + bf16_to_f32(ww[q] & 0xffffu) : 1.0f;
+            const float f1 = NORM ? 1.0f + bf16_to_f32(ww[q] >> 16) : 1.0f;
+            big = fmaxf(big, fmaxf(fabsf(a0 * f0), fabsf(a1 * f1)));
+        }
+    }
+    float r = 1.0f;
+    if (NORM) r = rms_inv(wave_sum(ss), K, eps);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+    big *= NORM ? r : 1.0f;
+    // the largest output is below big * (1 + 2^-8) (one bf16 rounding)
+    int e = 0;
+    while (!(big * 1.01f < 32768.0f * __builtin_ldexpf(1.0f, e)) && e < 200) ++e;
+    const float down = __builtin_ldexpf(1.0f, -e);
+    if (lane == 0) xscale[m] = __builtin_ldexpf(1.0f, e);
+    for (int c = lane; c < CH; c += 64) {
+        uint4 v = src[c];
+        if (NORM) {
+            const uint4 w = reinterpret_cast<const uint4*>(nw)[c];
+            v = make_uint4(norm_word(v.x, w.x, r), norm_word(v.y, w.y, r), norm_word(v.z, w.z, r),
+                           norm_word(v.w, w.w, r));
+        }
+        uint32_t pr[4];
+        pair_chunk(v, pr, 0.0f);
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const h2_t hv = {(_Float16)(bf16_to_f32(pr[q] & 0xffffu) * down),
+                             (_Float16)(bf16_to_f32(pr[q] >> 16) * down)};
+            o[q] = __builtin_bit_cast(uint32_t, hv);
+        }
+        dst[c] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+}  // namespace g16
+
+int launch_pair_rows16(const uint16_t* x, int M, int K, const uint16_t* norm_w, float eps, uint16_t* xp,
+                       float* xscale, hipStream_t st) {
+    if (M < 1 || K % 512 != 0) return -1;
+    const unsigned blocks = (unsigned)((M + 3) / 4);
+    if (norm_w)
+        hipLaunchKernelGGL(g16::pair_rows16_kernel<true>, dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps, xp,
+                           xscale);
+    else
+        hipLaunchKernelGGL(g16::pair_rows16_kernel<false>, dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps, xp,
+                           xscale);
+    return 0;
+}
+
+int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
+    // 32-bit byte offsets in the kernel; whole blocks of 8 groups (K % 512,
+    // the scale/bias DMA) with scale/bias rows 16-byte aligned
+    const bool fits32 = (int64_t)a.M * a.K * 2 <= 0xFFFFFFFFLL && (int64_t)a.N * a.K / 2 <= 0xFFFFFFFFLL;
+    auto a16 = [](const QMat& q) { return reinterpret_cast<uintptr_t>(q.s) % 16 == 0 && reinterpret_cast<uintptr_t>(q.b) % 16 == 0; };
+    if (!fits32 || a.K % 512 != 0 || a.M < 1 || a.N < 1 || !a16(a.A) || (epi == GEMM_SWIGLU && !a16(a.B))) return -1;
+    if (a.ysum && (epi != GEMM_SWIGLU || a.N % 128 != 0)) return -1;
+    const int BN = epi == GEMM_SWIGLU ? g16::BNW / 2 : g16::BNW;
+    const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + g16::TBM - 1) / g16::TBM));
+    switch (epi) {
+        case GEMM_STORE:
+            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_STORE>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
+            return 0;
+        case GEMM_STORE_F32:
+            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_STORE_F32>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
+            return 0;
+        case GEMM_RESIDUAL:
+            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_RESIDUAL>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
+            return 0;
+        case GEMM_SWIGLU:
+            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_SWIGLU>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
+            return 0;
+        default:
+            return -1;
+    }
+}
+
+}  // namespace mq4

@@ -834,11 +834,24 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
         D{down_wq, down_scales, down_biases};
     hipStream_t st = as_stream(stream);
     if (mlp_paired_ok(M, K, N, G, U, D)) {
-        if (launch_pair_rows(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
-            return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
-        // gate/up + SwiGLU writes h already paired, with its group sums
-        GemmArgs gu{w.xp, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, nullptr, 0.0f, w.xs, w.hs};
-        if (launch_q4_gemm(gu, GEMM_SWIGLU, false, st)) return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+        // gate/up + SwiGLU on an fp16 copy of the normalized x (its per-row
+        // power-of-two scales in the xs area) with the weights dequantized to
+        // fp16 (mq4_gemm16.hip); it writes h paired, with its group sums
+        // (scales and biases 16-byte aligned; else the exact-operand GEMM)
+        const bool f16_ok = aligned(G.s, 16) && aligned(G.b, 16) && aligned(U.s, 16) && aligned(U.b, 16);
+        if (f16_ok) {
+            if (launch_pair_rows16(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
+                return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+            Gemm16Args gu{w.xp, w.xs, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, w.hs};
+            if (launch_q4_gemm16(gu, GEMM_SWIGLU, st))
+                return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+        } else {
+            if (launch_pair_rows(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
+                return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+            GemmArgs gu{w.xp, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, nullptr, 0.0f, w.xs, w.hs};
+            if (launch_q4_gemm(gu, GEMM_SWIGLU, false, st))
+                return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+        }
         GemmArgs dn{w.hp, (int)M, (int)K, (int)N, D, QMat{nullptr, nullptr, nullptr}, y, x, nullptr, 0.0f, w.hs, nullptr};
         if (launch_q4_gemm(dn, GEMM_RESIDUAL, false, st)) return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
         return launch_status(what);
