@@ -39,9 +39,14 @@ struct GemmArgs {
 int launch_q4_gemm(const GemmArgs& a, int epi, bool norm, hipStream_t st);
 
 // The fp16-weight GEMM (mq4_gemm16.hip): x holds fp16 activations in the
-// operand order of launch_pair_rows16, row m scaled by 1 / xscale[m] (null:
-// 1), and the product of row m is multiplied by xscale[m].  Epilogues as
-// GemmArgs (GEMM_SWIGLU with ysum: N % 128 == 0).
+// operand order of launch_pair_rows16, row m scaled by 1 / (xscale[m] *
+// ascale) (xscale null: 1; ascale 0: 1), and the product of row m is
+// multiplied back by xscale[m] * ascale (powers of two).  Epilogues as
+// GemmArgs, plus:
+//  * GEMM_SWIGLU with yscale != 0: y = fp16(h * yscale) in the operand order
+//    (h the bf16 SwiGLU value; saturated at +-65504), no ysum; with
+//    yscale == 0 and ysum: the bf16 paired h and its group sums (N % 128 ==
+//    0), as GemmArgs.
 struct Gemm16Args {
     const uint16_t* x;       // [M, K] fp16, operand order
     const float* xscale;     // [M] powers of two, or null
@@ -50,6 +55,8 @@ struct Gemm16Args {
     void* y;
     const uint16_t* res;
     float* ysum;
+    float ascale;            // a power of two, or 0 (1)
+    float yscale;            // GEMM_SWIGLU: fp16 output scale, or 0 (bf16 output)
 };
 
 // Enqueue the fp16-weight GEMM; 0, or -1 for shapes it does not take (K % 512

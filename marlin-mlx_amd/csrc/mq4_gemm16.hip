@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
         wait_vmcnt<0>();
         lds_barrier();                               // group g is in `cur` for every wave
         const Wts wt = load_wts(g, cur);
-        issue(g + 1 < G ? g + 1 : G - 1, nxt);       // into the stage read in step g - 1
+        issue(g + 1 < G ? g + 1 : g, nxt);           // into the stage read in step g - 1
         if ((g & 7) == 0 && g + 8 < G) issue_sb((g >> 3) + 1, ((g >> 3) & 1) ? sb0 : sb1);
         compute(wt, cur);
     };
@@ -296,7 +296,8 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     // SwiGLU with ysum: h goes out in the operand order (column c of a chunk
     // at 2 (c % 4) + c / 4) and the group sums of its rows through LDS, 64
     // rows at a time (stage 0, free once every wave is past its last group)
-    const bool paired_out = EPI == GEMM_SWIGLU && p.ysum != nullptr;
+    const bool f16_out = EPI == GEMM_SWIGLU && p.yscale != 0.0f;
+    const bool paired_out = EPI == GEMM_SWIGLU && !f16_out && p.ysum != nullptr;
     constexpr int TS = BN + 8;                                     // bf16 per epilogue tile row
     uint16_t* tile = reinterpret_cast<uint16_t*>(&st0);          // [64][TS] bf16
     static_assert(64 * (BNW / 2 + 8) * 2 <= (int)sizeof(Stage), "epilogue tile");
@@ -305,12 +306,12 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int row = m0 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
-            sc[e] = p.xscale && row < M ? p.xscale[row] : 1.0f;
+            sc[e] = (p.xscale && row < M ? p.xscale[row] : 1.0f) * (p.ascale != 0.0f ? p.ascale : 1.0f);
         }
 #pragma unroll
         for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
             const int cn = NMAT == 2 ? n0 + wave * 32 + col : n0 + wave * 64 + j * 32 + col;
-            const int cw = paired_out ? ((cn & ~7) | (2 * (cn & 3) + ((cn >> 2) & 1))) : cn;
+            const int cw = paired_out || f16_out ? ((cn & ~7) | (2 * (cn & 3) + ((cn >> 2) & 1))) : cn;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int rl = i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
@@ -318,7 +319,15 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                 if (EPI == GEMM_SWIGLU) {
                     const uint32_t v = swiglu_bf16(acc[i][0][e] * sc[e], acc[i][1][e] * sc[e]);
                     if (paired_out) tile[(rl - rbase) * TS + wave * 32 + col] = (uint16_t)v;
-                    if (row < M && cn < N) reinterpret_cast<uint16_t*>(p.y)[(int64_t)row * N + cw] = (uint16_t)v;
+                    if (row < M && cn < N) {
+                        uint16_t o = (uint16_t)v;
+                        if (f16_out) {
+                            // exact for |h| within [2^-14, 65504] / yscale
+                            const float hv = fminf(fmaxf(bf16_to_f32(v) * p.yscale, -65504.0f), 65504.0f);
+                            o = __builtin_bit_cast(uint16_t, (_Float16)hv);
+                        }
+                        reinterpret_cast<uint16_t*>(p.y)[(int64_t)row * N + cw] = o;
+                    }
                     continue;
                 }
                 if (row >= M || cn >= N) continue;
@@ -461,7 +470,8 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
     const bool fits32 = (int64_t)a.M * a.K * 2 <= 0xFFFFFFFFLL && (int64_t)a.N * a.K / 2 <= 0xFFFFFFFFLL;
     auto a16 = [](const QMat& q) { return reinterpret_cast<uintptr_t>(q.s) % 16 == 0 && reinterpret_cast<uintptr_t>(q.b) % 16 == 0; };
     if (!fits32 || a.K % 512 != 0 || a.M < 1 || a.N < 1 || !a16(a.A) || (epi == GEMM_SWIGLU && !a16(a.B))) return -1;
-    if (a.ysum && (epi != GEMM_SWIGLU || a.N % 128 != 0)) return -1;
+    if (a.ysum && (epi != GEMM_SWIGLU || a.yscale != 0.0f || a.N % 128 != 0)) return -1;
+    if (a.yscale != 0.0f && (epi != GEMM_SWIGLU || a.N % 8 != 0)) return -1;
     const int BN = epi == GEMM_SWIGLU ? g16::BNW / 2 : g16::BNW;
     const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + g16::TBM - 1) / g16::TBM));
     switch (epi) {

@@ -834,20 +834,37 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
         D{down_wq, down_scales, down_biases};
     hipStream_t st = as_stream(stream);
     if (mlp_paired_ok(M, K, N, G, U, D)) {
-        // gate/up + SwiGLU on an fp16 copy of the normalized x (its per-row
-        // power-of-two scales in the xs area) with the weights dequantized to
-        // fp16 (mq4_gemm16.hip); it writes h paired, with its group sums
-        // (scales and biases 16-byte aligned; else the exact-operand GEMM)
-        const bool f16_ok = aligned(G.s, 16) && aligned(G.b, 16) && aligned(U.s, 16) && aligned(U.b, 16);
-        if (f16_ok) {
+        // The fp16-weight GEMM (mq4_gemm16.hip) when every scale and bias row
+        // is 16-byte aligned (else the exact-operand GEMM below): gate/up +
+        // SwiGLU on an fp16 copy of the normalized x (its per-row
+        // power-of-two scales in the xs area).  When the down product gives
+        // at least two 128 x 256 blocks per CU it runs on the fp16 GEMM too,
+        // on h written as fp16 / 256 in the operand order (exact for |h| in
+        // [2^-6, 1.6e7]); otherwise gate/up writes h paired in bf16 with its
+        // group sums for the exact-operand GEMM's 64 x 32 wave tiles (at M =
+        // 2048 one fp16 block per CU, or two K parts and a combine, measured
+        // slower: 231 against 223 us for the MLP half)
+        auto a16 = [](const QMat& q) { return aligned(q.s, 16) && aligned(q.b, 16); };
+        if (a16(G) && a16(U)) {
+            const bool down16 = a16(D) && (N / 64) % 8 == 0 &&
+                                ((M + 127) / 128) * ((K + 255) / 256) >= 2 * (int64_t)num_cus();
             if (launch_pair_rows16(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
-            Gemm16Args gu{w.xp, w.xs, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, w.hs};
+            Gemm16Args gu{w.xp, w.xs, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, down16 ? nullptr : w.hs, 0.0f,
+                          down16 ? 1.0f / 256.0f : 0.0f};
             if (launch_q4_gemm16(gu, GEMM_SWIGLU, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+            if (down16) {
+                Gemm16Args dn{w.hp, nullptr, (int)M, (int)K, (int)N, D, QMat{nullptr, nullptr, nullptr}, y, x,
+                              nullptr, 256.0f, 0.0f};
+                if (launch_q4_gemm16(dn, GEMM_RESIDUAL, st))
+                    return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+                return launch_status(what);
+            }
         } else {
             if (launch_pair_rows(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
+            // gate/up + SwiGLU writes h already paired, with its group sums
             GemmArgs gu{w.xp, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, nullptr, 0.0f, w.xs, w.hs};
             if (launch_q4_gemm(gu, GEMM_SWIGLU, false, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);

@@ -233,6 +233,8 @@ def test_mlp_residual_workspace_and_validation(mq4):
     assert L.mq4_mlp_workspace_size(16, 2048, 6144) == up(16 * 6144 * 2) + up(2 * 16 * 2048 * 4)
     assert L.mq4_mlp_workspace_size(32, 2048, 6144) == up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
     M, K, N = 2048, 2048, 6144
+    # from 33 rows: h, the paired (or fp16) operand, its group sums (or row
+    # scales) and h's group sums
     assert L.mq4_mlp_workspace_size(M, K, N) == up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) + up(M * N // 64 * 4)
     # the size for M rows covers every call of at most M rows (the paired
     # GEMM regime from 33 rows needs less per row than the two fp32 K parts of

@@ -212,10 +212,13 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     a combine (72 and 80 groups: the second part partly empty), and (70, 640,
     1280) the separate GEMM kernels.
     * Against the separate entries (mq4_rmsnorm_gate_up_silu +
-      mq4_qmm_residual, each pinned to the oracle): the same normalized
-      operand and bf16 h, fp32 sums in another order, so >= 98% of outputs
-      bit-identical and rms of the difference of the MLP parts <= 1e-2 of rms;
-      on the GEMV path bit for bit.
+      mq4_qmm_residual, each pinned to the oracle): rms of the difference of
+      the MLP parts <= 1e-2 of rms; on the GEMV path bit for bit.  From 33
+      rows with 16-byte aligned scales and biases the one call runs the
+      fp16-weight GEMM (weights fp16(s q + b), about 2e-6 of the output rms
+      from the exact product), whose gate/up flips the bf16 rounding of about
+      1-2% of h: >= 95% of the outputs bit-identical (measured ~98%, rms of
+      the difference ~8e-4).
     * Against the oracle's chain (rms_norm, gate/up, bf16 SwiGLU, fp64 down,
       bf16 residual add) on sampled rows: rms(err) <= 1e-2 x rms of the
       oracle's MLP output."""
@@ -240,7 +243,7 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     print(f"vs separate entries: identical {same:.5f}, rms(diff)/rms(mlp) {rel:.2e}")
     if M < 33:
         assert np.array_equal(got, sep)
-    assert same >= 0.98 and rel <= TOL
+    assert same >= 0.95 and rel <= TOL
     rows = sampled_rows(M) if M > 64 else np.arange(M)
     rows = rows[(rows >= 0) & (rows < M)]
     xs = xh[rows]
