@@ -52,7 +52,14 @@
 //  * The operand layout is mq4_gemm.hip's: lane l of a tile holds row (or
 //    weight column) l % 32 and k-half l / 32; MFMA step ks takes word ks of
 //    the half, whose nibble pairs (q_p, q_{p+4}) meet the activations in the
-//    pair order (x_p, x_{p+4}) of the pre-pass.
+//    pair order (x_p, x_{p+4}) of the pre-pass.  The weights are the MFMA's
+//    row operand and the activations its column operand, so that a result
+//    lane holds one activation row and four runs of four consecutive weight
+//    columns: the epilogue reads one row scale per 32 rows and writes 8-byte
+//    runs.  (With the activations as the row operand a lane held one column
+//    of 16 rows: a row-scale load and a 2-byte store per output, which cost
+//    the SwiGLU product 26 us of 72 at M = 2048 in a copy without the
+//    dequantization and the data movement.)
 #include <type_traits>
 
 #include "mq4_device.h"
@@ -119,6 +126,10 @@ __device__ __forceinline__ h8_t dequant_word(uint32_t w, h2_t s2, h2_t b2, uint3
     }
     return __builtin_bit_cast(h8_t, make_uint4(out[0], out[1], out[2], out[3]));
 }
+
+// Column of an 8-column chunk whose pair-order position (2 (c % 4) + c / 4)
+// is r.
+__device__ __forceinline__ int perm8(int r) { return 4 * (r & 1) + (r >> 1); }
 
 // MFMA results are read by the VALU only in the epilogue; the padding keeps
 // the wait states between the last MFMA and that read generous.
@@ -207,9 +218,16 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     };
 
     // ---- this lane's weight columns (block-relative) of tiles j = 0, 1 ----
+    // Weight column c of a tile is MFMA row c, except for outputs in the
+    // pair order: there MFMA row 8 b + r holds column 8 b + perm8(r), so that
+    // the four consecutive MFMA rows of a result lane are four consecutive
+    // positions of the pair order.
+    const bool f16_out = EPI == GEMM_SWIGLU && p.yscale != 0.0f;
+    const bool paired_out = EPI == GEMM_SWIGLU && !f16_out && p.ysum != nullptr;
+    const int ccol = f16_out || paired_out ? ((col & ~7) | perm8(col & 7)) : col;
     int wr[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wave * 32 + col : wave * 64 + j * 32 + col;
+    for (int j = 0; j < 2; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wave * 32 + ccol : wave * 64 + j * 32 + ccol;
 
     uint32_t nib_mask, nib_exp;               // the nibble-pair constants, set up once
     asm("s_mov_b32 %0, 0x000f000f" : "=s"(nib_mask));
@@ -243,29 +261,61 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
         }
         return w;
     };
+    // The weights are the MFMA row operand and the activations the column
+    // operand: result lane l of tile (i, j) holds activation row i 32 + l % 32.
+    // MFMA step ks + 1's activation reads and dequantization are issued
+    // during step ks's MFMAs (two operand sets), one MFMA per LDS read and
+    // four VALU.
     auto compute = [&](const Wts& wt, const Stage& st) {
         const uint4* bw = wt.bw;
         const h2_t* s2 = wt.s2;
         const h2_t* b2 = wt.b2;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            h8_t a[4], bo[2];
+        auto read_a = [&](int ks, h8_t (&a)[4]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = i * 32 + col, ch = 4 * h + ks;
                 a[i] = __builtin_bit_cast(h8_t, st.a[r * 8 + (ch ^ ((r >> 1) & 7))]);
             }
+        };
+        auto dequant = [&](int ks, h8_t (&bo)[2]) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const uint32_t w = ks == 0 ? bw[j].x : ks == 1 ? bw[j].y : ks == 2 ? bw[j].z : bw[j].w;
                 bo[j] = dequant_word(w, s2[j], b2[j], nib_mask, nib_exp);
             }
+        };
+        auto mfmas = [&](const h8_t (&a)[4], const h8_t (&bo)[2]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bo[j], acc[i][j], 0, 0, 0);
-        }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bo[j], a[i], acc[i][j], 0, 0, 0);
+        };
+        auto interleave = [] {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
+                if (m < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                 // VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        h8_t a0[4], a1[4], w0[2], w1[2];
+        read_a(0, a0);
+        dequant(0, w0);
+        read_a(1, a1);
+        dequant(1, w1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(a0, w0);
+        read_a(2, a0);
+        dequant(2, w0);
+        interleave();
+        mfmas(a1, w1);
+        read_a(3, a1);
+        dequant(3, w1);
+        interleave();
+        mfmas(a0, w0);
+        mfmas(a1, w1);
     };
     // Two stages: step g waits for all of this wave's DMA (group g's), meets
     // the other waves at the barrier, reads group g's weights, issues group
@@ -292,54 +342,95 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     wait_vmcnt<0>();                                 // no DMA outstanding past the loop
     mfma_result_pad();
 
-    // ---- epilogue: lane l of a 32 x 32 tile holds rows (e/4)*8 + (l/32)*4 + e%4, column l%32 ----
-    // SwiGLU with ysum: h goes out in the operand order (column c of a chunk
-    // at 2 (c % 4) + c / 4) and the group sums of its rows through LDS, 64
-    // rows at a time (stage 0, free once every wave is past its last group)
-    const bool f16_out = EPI == GEMM_SWIGLU && p.yscale != 0.0f;
-    const bool paired_out = EPI == GEMM_SWIGLU && !f16_out && p.ysum != nullptr;
+    // ---- epilogue: result lane l of tile (i, j) holds activation row
+    // i 32 + l % 32 and MFMA rows (e / 4) 8 + (l / 32) 4 + e % 4 of tile j:
+    // four runs of four consecutive output columns (natural order, or the
+    // pair-order positions 4 (l / 32) .. + 3 of an 8-column chunk), each
+    // stored as one 8-byte (16 for fp32) write.
+    // SwiGLU with ysum: h also goes to an LDS tile in natural column order,
+    // 64 rows at a time (stage 0, free once every wave is past its last
+    // group), for the group sums of its rows.
     constexpr int TS = BN + 8;                                     // bf16 per epilogue tile row
     uint16_t* tile = reinterpret_cast<uint16_t*>(&st0);          // [64][TS] bf16
     static_assert(64 * (BNW / 2 + 8) * 2 <= (int)sizeof(Stage), "epilogue tile");
+    // whole-run vector stores: N % 4 == 0 and 8-byte (fp32: 16-byte) aligned y and res
+    const bool vec = N % 4 == 0 && reinterpret_cast<uintptr_t>(p.y) % (EPI == GEMM_STORE_F32 ? 16 : 8) == 0 &&
+                     (EPI != GEMM_RESIDUAL || reinterpret_cast<uintptr_t>(p.res) % 8 == 0);
+    const float ascale = p.ascale != 0.0f ? p.ascale : 1.0f;
     auto emit = [&](int i, int rbase) {
-        float sc[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int row = m0 + i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
-            sc[e] = (p.xscale && row < M ? p.xscale[row] : 1.0f) * (p.ascale != 0.0f ? p.ascale : 1.0f);
-        }
+        const int rl = i * 32 + col, row = m0 + rl;
+        if (row >= M) return;
+        const float sc = (p.xscale ? p.xscale[row] : 1.0f) * ascale;
+        const int64_t rowo = (int64_t)row * N;
 #pragma unroll
         for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
-            const int cn = NMAT == 2 ? n0 + wave * 32 + col : n0 + wave * 64 + j * 32 + col;
-            const int cw = paired_out || f16_out ? ((cn & ~7) | (2 * (cn & 3) + ((cn >> 2) & 1))) : cn;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int rl = i * 32 + (e >> 2) * 8 + h * 4 + (e & 3);
-                const int row = m0 + rl;
+            for (int eg = 0; eg < 4; ++eg) {
+                const int cl = (NMAT == 2 ? wave * 32 : wave * 64 + j * 32) + eg * 8 + h * 4;
+                const int cb = n0 + cl;                             // first column (position) of the run
+                if (cb >= N) continue;
+                const bool whole = vec && cb + 3 < N;
                 if (EPI == GEMM_SWIGLU) {
-                    const uint32_t v = swiglu_bf16(acc[i][0][e] * sc[e], acc[i][1][e] * sc[e]);
-                    if (paired_out) tile[(rl - rbase) * TS + wave * 32 + col] = (uint16_t)v;
-                    if (row < M && cn < N) {
-                        uint16_t o = (uint16_t)v;
+                    uint32_t o[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t v = swiglu_bf16(acc[i][0][eg * 4 + q] * sc, acc[i][1][eg * 4 + q] * sc);
+                        o[q] = v;
+                        if (paired_out) tile[(rl - rbase) * TS + (cl & ~7) + perm8(h * 4 + q)] = (uint16_t)v;
                         if (f16_out) {
                             // exact for |h| within [2^-14, 65504] / yscale
                             const float hv = fminf(fmaxf(bf16_to_f32(v) * p.yscale, -65504.0f), 65504.0f);
-                            o = __builtin_bit_cast(uint16_t, (_Float16)hv);
+                            o[q] = __builtin_bit_cast(uint16_t, (_Float16)hv);
                         }
-                        reinterpret_cast<uint16_t*>(p.y)[(int64_t)row * N + cw] = o;
+                    }
+                    uint16_t* y = reinterpret_cast<uint16_t*>(p.y) + rowo + cb;
+                    if (whole) {
+                        *reinterpret_cast<uint2*>(y) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (cb + q < N) y[q] = (uint16_t)o[q];
                     }
                     continue;
                 }
-                if (row >= M || cn >= N) continue;
-                const int64_t o = (int64_t)row * N + cn;
-                const float v = acc[i][j][e] * sc[e];
+                float v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = acc[i][j][eg * 4 + q] * sc;
+                if (EPI == GEMM_STORE_F32) {
+                    float* y = reinterpret_cast<float*>(p.y) + rowo + cb;
+                    if (whole) {
+                        *reinterpret_cast<float4*>(y) = make_float4(v[0], v[1], v[2], v[3]);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (cb + q < N) y[q] = v[q];
+                    }
+                    continue;
+                }
+                uint32_t o[4];
+                uint16_t* y = reinterpret_cast<uint16_t*>(p.y) + rowo + cb;
                 if (EPI == GEMM_STORE) {
-                    reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)f32_to_bf16(v);
-                } else if (EPI == GEMM_STORE_F32) {
-                    reinterpret_cast<float*>(p.y)[o] = v;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) o[q] = f32_to_bf16(v[q]);
                 } else {
-                    reinterpret_cast<uint16_t*>(p.y)[o] =
-                        (uint16_t)f32_to_bf16(bf16_to_f32(p.res[o]) + round_bf16(v));
+                    const uint16_t* r = p.res + rowo + cb;
+                    uint32_t rv[4];
+                    if (whole) {
+                        const uint2 t = *reinterpret_cast<const uint2*>(r);
+                        rv[0] = t.x & 0xffffu; rv[1] = t.x >> 16; rv[2] = t.y & 0xffffu; rv[3] = t.y >> 16;
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) rv[q] = cb + q < N ? r[q] : 0u;
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) o[q] = f32_to_bf16(bf16_to_f32(rv[q]) + round_bf16(v[q]));
+                }
+                if (whole) {
+                    *reinterpret_cast<uint2*>(y) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (cb + q < N) y[q] = (uint16_t)o[q];
                 }
             }
         }
