@@ -27,6 +27,8 @@ CPP_DEMO_SRC = os.path.join(ROOT, "tests", "cpp", "mq4_cpp_demo.cpp")
 CPP_DEMO = os.path.join(BUILD, "mq4_cpp_demo")
 CACHE_TOOL_SRC = os.path.join(ROOT, "tests", "cpp", "mq4_cache_tool.cpp")
 CACHE_TOOL = os.path.join(BUILD, "mq4_cache_tool")
+DEVCHECK_SRC = os.path.join(ROOT, "tests", "hip", "mq4_device_check.hip")
+DEVCHECK = os.path.join(BUILD, "libmq4_devcheck.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -128,6 +130,12 @@ def build(verbose: bool = True) -> str:
         p = subprocess.run(cmd, capture_output=True, text=True)
         if p.returncode != 0:
             raise RuntimeError("C++ cache tool build failed:\n" + p.stderr)
+    if os.path.exists(DEVCHECK_SRC):
+        # device-helper checks for the tests (tests/hip), with the library's flags
+        cmd = [HIPCC, *CFLAGS, "-shared", DEVCHECK_SRC, "-o", DEVCHECK]
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        if p.returncode != 0:
+            raise RuntimeError("device check build failed:\n" + p.stderr)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
     return LIB

@@ -142,6 +142,50 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float g_acc, float u_acc) {
     return f32_to_bf16(t * u);
 }
 
+// round_bf16(1 / (1 + expf(-g))) for a bf16 value g, bit for bit, mostly
+// without expf and the IEEE division.  exp(-g) = 2^(xh + xl) with the
+// Cody-Waite split xh = -g L_HI (exact: 8 x 15 significant bits), xl = -g
+// L_LO; 2^xh on v_exp_f32, 2^xl = 1 + t + t^2 / 2 (t = xl ln 2, |t| < 2^-10
+// for |g| < 64); the reciprocal of 1 + e on v_rcp_f32 plus one Newton step.
+// That value r is within a few fp32 ulps of the exact formula's, so both
+// round to the same bf16 unless r's low 16 bits lie within SIG_MARGIN of
+// the rounding midpoint 0x8000; then, and for |g| >= 64 or non-finite g,
+// the exact formula is evaluated.  Checked against it for all 65536 bf16
+// values of g (tests/hip/mq4_device_check.hip).
+constexpr uint32_t SIG_MARGIN = 16;
+__device__ __forceinline__ bool sigmoid_bf16_fast(float g, float& s) {
+#pragma clang fp contract(off)
+    constexpr float L_HI = 0x1.7154p+0f;               // log2(e) to 15 significant bits
+    constexpr float L_LO = 0x1.d94ae0p-18f;            // log2(e) - L_HI
+    constexpr float LN2 = 0x1.62e430p-1f;
+    const float xh = -g * L_HI;
+    const float t = (-g * L_LO) * LN2;
+    float e = __builtin_amdgcn_exp2f(xh);
+    e = __builtin_fmaf(e, t + 0.5f * t * t, e);
+    const float d = 1.0f + e;
+    float r = __builtin_amdgcn_rcpf(d);
+    r = __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
+    const uint32_t lo = __builtin_bit_cast(uint32_t, r) & 0xffffu;
+    const uint32_t dist = lo > 0x8000u ? lo - 0x8000u : 0x8000u - lo;
+    s = round_bf16(r);
+    return __builtin_fabsf(g) < 64.0f && dist > SIG_MARGIN;
+}
+__device__ __forceinline__ float sigmoid_bf16(float g) {
+#pragma clang fp contract(off)
+    float s;
+    if (!sigmoid_bf16_fast(g, s)) s = round_bf16(1.0f / (1.0f + expf(-g)));
+    return s;
+}
+
+// swiglu_bf16 with sigmoid_bf16: the same bits.
+__device__ __forceinline__ uint32_t swiglu_bf16_fast(float g_acc, float u_acc) {
+#pragma clang fp contract(off)
+    const float g = round_bf16(g_acc);
+    const float u = round_bf16(u_acc);
+    const float t = round_bf16(sigmoid_bf16(g) * g);
+    return f32_to_bf16(t * u);
+}
+
 // Monotone 16-bit key of a bf16 value for max-selection: larger value ->
 // larger key; -0 maps like +0 and NaN maps to 0 (below every number).
 __device__ __forceinline__ uint32_t bf16_order_key(uint32_t h) {

@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                     uint32_t o[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const uint32_t v = swiglu_bf16(acc[i][0][eg * 4 + q] * sc, acc[i][1][eg * 4 + q] * sc);
+                        const uint32_t v = swiglu_bf16_fast(acc[i][0][eg * 4 + q] * sc, acc[i][1][eg * 4 + q] * sc);
                         o[q] = v;
                         if (paired_out) tile[(rl - rbase) * TS + (cl & ~7) + perm8(h * 4 + q)] = (uint16_t)v;
                         if (f16_out) {
