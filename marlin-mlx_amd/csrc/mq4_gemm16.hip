@@ -151,6 +151,16 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, col = lane & 31;
     const int M = p.M, N = p.N, K = p.K, G = K / 64;
+    // K parts (GEMM_RESIDUAL): block b takes part b / tiles, groups
+    // [part GL, (part + 1) GL), and writes its fp32 partial product
+    const int S = EPI == GEMM_RESIDUAL && p.ksplit > 1 ? p.ksplit : 1;
+    const int GL = G / S;
+    int bt = blockIdx.x, kpart = 0;
+    if (S > 1) {
+        const int tiles = (int)gridDim.x / S;
+        kpart = bt / tiles;
+        bt -= kpart * tiles;
+    }
 
     // XCD-aware block order: with the column blocks a multiple of 8, XCD x
     // (block b runs on XCD b % 8) takes a fixed eighth of them for every row
@@ -158,7 +168,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     const int NB = (N + BN - 1) / BN;
     int nb, mb;
     {
-        const int b = blockIdx.x;
+        const int b = bt;
         if ((NB & 7) == 0) {
             const int per = NB >> 3, s = b >> 3;
             nb = (s % per) * 8 + (b & 7);
@@ -171,7 +181,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     const int n0 = nb * BN, m0 = mb * TBM;
 
     // ---- DMA sources: wave-uniform bases plus 32-bit lane byte offsets ----
-    const char* const xbase = reinterpret_cast<const char*>(p.x);
+    const char* const xbase = reinterpret_cast<const char*>(p.x) + (int64_t)kpart * GL * 128;
     uint32_t aoff[A_I];
 #pragma unroll
     for (int t = 0; t < A_I; ++t) {
@@ -194,7 +204,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
 #pragma unroll
     for (int t = 0; t < B_I; ++t) {
         const int q0 = (wave * B_I + t) * 64, r0 = q0 >> 1;
-        bbase[t] = reinterpret_cast<const char*>(mat_of(r0).wq);
+        bbase[t] = reinterpret_cast<const char*>(mat_of(r0).wq) + (int64_t)kpart * GL * 32;
         boff[t] = (uint32_t)((int64_t)wrow_of(r0 + (lane >> 1)) * (K / 2) + (lane & 1) * 16);
     }
     // scales and biases: 16 bytes (8 groups) of one weight column per lane
@@ -203,7 +213,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
 #pragma unroll
     for (int t = 0; t < SB_I; ++t) {
         const int u0 = (wave * SB_I + t) * 64, sel = u0 / BNW, r0 = u0 % BNW;
-        sbbase[t] = reinterpret_cast<const char*>(sel ? mat_of(r0).b : mat_of(r0).s);
+        sbbase[t] = reinterpret_cast<const char*>(sel ? mat_of(r0).b : mat_of(r0).s) + (int64_t)kpart * (GL / 8) * 16;
         sboff[t] = (uint32_t)((int64_t)wrow_of(r0 + lane) * G * 2);
     }
     auto issue = [&](int g, Stage& st) {
@@ -327,18 +337,18 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
         wait_vmcnt<0>();
         lds_barrier();                               // group g is in `cur` for every wave
         const Wts wt = load_wts(g, cur);
-        issue(g + 1 < G ? g + 1 : g, nxt);           // into the stage read in step g - 1
-        if ((g & 7) == 0 && g + 8 < G) issue_sb((g >> 3) + 1, ((g >> 3) & 1) ? sb0 : sb1);
+        issue(g + 1 < GL ? g + 1 : g, nxt);          // into the stage read in step g - 1
+        if ((g & 7) == 0 && g + 8 < GL) issue_sb((g >> 3) + 1, ((g >> 3) & 1) ? sb0 : sb1);
         compute(wt, cur);
     };
     issue(0, st0);
     issue_sb(0, sb0);
     int g0 = 0;
-    for (; g0 + 2 <= G; g0 += 2) {
+    for (; g0 + 2 <= GL; g0 += 2) {
         step(g0, st0, st1);
         step(g0 + 1, st1, st0);
     }
-    if (g0 < G) step(g0, st0, st1);
+    if (g0 < GL) step(g0, st0, st1);
     wait_vmcnt<0>();                                 // no DMA outstanding past the loop
     mfma_result_pad();
 
@@ -354,8 +364,10 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     uint16_t* tile = reinterpret_cast<uint16_t*>(&st0);          // [64][TS] bf16
     static_assert(64 * (BNW / 2 + 8) * 2 <= (int)sizeof(Stage), "epilogue tile");
     // whole-run vector stores: N % 4 == 0 and 8-byte (fp32: 16-byte) aligned y and res
-    const bool vec = N % 4 == 0 && reinterpret_cast<uintptr_t>(p.y) % (EPI == GEMM_STORE_F32 ? 16 : 8) == 0 &&
-                     (EPI != GEMM_RESIDUAL || reinterpret_cast<uintptr_t>(p.res) % 8 == 0);
+    const bool vec = N % 4 == 0 &&
+                     (S > 1 ? reinterpret_cast<uintptr_t>(p.part) % 16 == 0
+                            : reinterpret_cast<uintptr_t>(p.y) % (EPI == GEMM_STORE_F32 ? 16 : 8) == 0 &&
+                                  (EPI != GEMM_RESIDUAL || reinterpret_cast<uintptr_t>(p.res) % 8 == 0));
     const float ascale = p.ascale != 0.0f ? p.ascale : 1.0f;
     auto emit = [&](int i, int rbase) {
         const int rl = i * 32 + col, row = m0 + rl;
@@ -396,8 +408,8 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                 float v[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) v[q] = acc[i][j][eg * 4 + q] * sc;
-                if (EPI == GEMM_STORE_F32) {
-                    float* y = reinterpret_cast<float*>(p.y) + rowo + cb;
+                if (EPI == GEMM_STORE_F32 || S > 1) {
+                    float* y = (S > 1 ? p.part + (int64_t)kpart * M * N : reinterpret_cast<float*>(p.y)) + rowo + cb;
                     if (whole) {
                         *reinterpret_cast<float4*>(y) = make_float4(v[0], v[1], v[2], v[3]);
                     } else {
@@ -540,6 +552,32 @@ __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __rest
     }
 }
 
+// y = bf16(res + round_bf16(part[0] + part[1] + ... + part[S - 1])), the
+// parts added in order: 4 elements per thread (MN % 4 == 0, 16-byte aligned
+// parts, 8-byte aligned res and y).
+__global__ __launch_bounds__(256) void kpart_residual_kernel(const float* __restrict__ part, int S, int64_t MN,
+                                                             const uint16_t* __restrict__ res,
+                                                             uint16_t* __restrict__ y) {
+#pragma clang fp contract(off)
+    const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e >= MN) return;
+    float4 sum = *reinterpret_cast<const float4*>(part + e);
+    for (int k = 1; k < S; ++k) {
+        const float4 v = *reinterpret_cast<const float4*>(part + (int64_t)k * MN + e);
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
+    }
+    const uint2 r = *reinterpret_cast<const uint2*>(res + e);
+    const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+    const uint32_t rv[4] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = f32_to_bf16(bf16_to_f32(rv[q]) + round_bf16(sv[q]));
+    *reinterpret_cast<uint2*>(y + e) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+}
+
 }  // namespace g16
 
 int launch_pair_rows16(const uint16_t* x, int M, int K, const uint16_t* norm_w, float eps, uint16_t* xp,
@@ -563,8 +601,16 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
     if (!fits32 || a.K % 512 != 0 || a.M < 1 || a.N < 1 || !a16(a.A) || (epi == GEMM_SWIGLU && !a16(a.B))) return -1;
     if (a.ysum && (epi != GEMM_SWIGLU || a.yscale != 0.0f || a.N % 128 != 0)) return -1;
     if (a.yscale != 0.0f && (epi != GEMM_SWIGLU || a.N % 8 != 0)) return -1;
+    // K parts: GEMM_RESIDUAL only, whole 8-group scale slots per part, fp32
+    // parts [ksplit][M][N] (16-byte aligned, N % 4 == 0) combined by a second
+    // kernel
+    const int S = a.ksplit > 1 ? a.ksplit : 1;
+    if (S > 1 && (epi != GEMM_RESIDUAL || (a.K / 64) % (8 * S) != 0 || !a.part ||
+                  reinterpret_cast<uintptr_t>(a.part) % 16 != 0 || a.N % 4 != 0 || !aligned(a.res, 8) ||
+                  !aligned(a.y, 8)))
+        return -1;
     const int BN = epi == GEMM_SWIGLU ? g16::BNW / 2 : g16::BNW;
-    const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + g16::TBM - 1) / g16::TBM));
+    const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + g16::TBM - 1) / g16::TBM) * S);
     switch (epi) {
         case GEMM_STORE:
             hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_STORE>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
@@ -572,9 +618,15 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
         case GEMM_STORE_F32:
             hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_STORE_F32>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
             return 0;
-        case GEMM_RESIDUAL:
+        case GEMM_RESIDUAL: {
             hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_RESIDUAL>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
+            if (S > 1) {
+                const int64_t MN = (int64_t)a.M * a.N;
+                hipLaunchKernelGGL(g16::kpart_residual_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,
+                                   st, a.part, S, MN, a.res, reinterpret_cast<uint16_t*>(a.y));
+            }
             return 0;
+        }
         case GEMM_SWIGLU:
             hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_SWIGLU>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
             return 0;

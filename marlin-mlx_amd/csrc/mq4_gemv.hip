@@ -753,8 +753,9 @@ namespace mq4 {
 // operand order by the SwiGLU epilogue, and the normalized x (by
 // launch_pair_rows) too, both with their fp32 group sums, so neither GEMM
 // forms them per wave.  On the MFMA GEMV path (kMfmaMinM <= M < kGemmMinM)
-// part [2, M, K] fp32 holds the two K parts of the split down product.
-// Sections 256-byte aligned.
+// part [2, M, K] fp32 holds the two K parts of the split down product.  On
+// the fp16-weight path the down product in S > 1 K parts puts them in
+// kpart [S, M, K] fp32.  Sections 256-byte aligned.
 struct MlpWs {
     uint16_t* h = nullptr;
     uint16_t* xp = nullptr;
@@ -762,8 +763,26 @@ struct MlpWs {
     uint16_t* hp = nullptr;
     float* hs = nullptr;
     float* part = nullptr;
+    float* kpart = nullptr;
     size_t bytes = 0;
 };
+
+// K parts of the fp16-weight down product ([M, N] . [K, N]^T, N / 64 groups)
+// on the one-call path: the most of 1, 2 and 4 (whole 8-group scale slots
+// per part) whose 128 x 256 tiles times parts stay within one block per CU.
+// Measured on the 2048 x 6144 down product with its part combine: M = 1024,
+// 64 tiles: 90 / 54 / 45 us for 1 / 2 / 4 parts; M = 2048, 128 tiles: 93 /
+// 71 / 75 us; M = 4096, 256 tiles: 121 / 124 / 141 us.  0: N / 64 not a
+// multiple of 8 (no fp16 down product).
+static int mlp_down_parts(int64_t M, int64_t K, int64_t N) {
+    const int64_t G = N / 64;
+    if (N % 64 != 0 || G % 8 != 0) return 0;
+    const int64_t tiles = ((M + 127) / 128) * ((K + 255) / 256);
+    int S = 1;
+    for (int s : {2, 4})
+        if ((G / 8) % s == 0 && tiles * s <= (int64_t)num_cus()) S = s;
+    return S;
+}
 
 static MlpWs mlp_ws_layout(void* base, int64_t M, int64_t K, int64_t N) {
     MlpWs w;
@@ -780,6 +799,8 @@ static MlpWs mlp_ws_layout(void* base, int64_t M, int64_t K, int64_t N) {
         w.xp = reinterpret_cast<uint16_t*>(take((size_t)M * K * 2));
         w.xs = reinterpret_cast<float*>(take((size_t)M * (K / 64) * 4));
         w.hs = reinterpret_cast<float*>(take((size_t)M * (N / 64) * 4));
+        const int S = mlp_down_parts(M, K, N);
+        if (S > 1) w.kpart = reinterpret_cast<float*>(take((size_t)S * M * K * 4));
     } else if (M >= kMfmaMinM) {
         w.part = reinterpret_cast<float*>(take((size_t)2 * M * K * 4));
     }
@@ -800,17 +821,22 @@ static bool mlp_paired_ok(int64_t M, int64_t K, int64_t N, const QMat& g, const 
 
 // Enough for every call of at most M rows: the layout's size grows with the
 // row count inside each of its three regimes (up to kMfmaMinM - 1 rows: h
-// only; to kGemmMinM - 1: h and two fp32 K parts; from kGemmMinM: h and the
-// paired operands), but the third regime needs less per row than the second,
-// so the size is the largest over the regimes' top row counts up to M.
+// only; to kGemmMinM - 1: h and two fp32 K parts; from kGemmMinM: h, the
+// paired operands and the down product's K parts), except where the K-part
+// count drops, so the size is the largest over the regimes' top row counts
+// and the row counts just below a drop (multiples of 128), up to M.
 extern "C" size_t mq4_mlp_workspace_size(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0) return 0;
     size_t need = mlp_ws_layout(nullptr, M, K, N).bytes;
-    for (int64_t top : {(int64_t)kMfmaMinM - 1, (int64_t)kGemmMinM - 1}) {
-        const int64_t m = top < M ? top : M;
+    auto at = [&](int64_t m) {
+        if (m < 1 || m > M) return;
         const size_t b = mlp_ws_layout(nullptr, m, K, N).bytes;
         need = b > need ? b : need;
-    }
+    };
+    at(kMfmaMinM - 1);
+    at(kGemmMinM - 1);
+    for (int64_t m = 128; m < M; m += 128)
+        if (mlp_down_parts(m, K, N) > mlp_down_parts(m + 1, K, N)) at(m);
     return need;
 }
 
@@ -837,17 +863,17 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
         // The fp16-weight GEMM (mq4_gemm16.hip) when every scale and bias row
         // is 16-byte aligned (else the exact-operand GEMM below): gate/up +
         // SwiGLU on an fp16 copy of the normalized x (its per-row
-        // power-of-two scales in the xs area).  When the down product gives
-        // at least two 128 x 256 blocks per CU it runs on the fp16 GEMM too,
-        // on h written as fp16 / 256 in the operand order (exact for |h| in
-        // [2^-6, 1.6e7]); otherwise gate/up writes h paired in bf16 with its
-        // group sums for the exact-operand GEMM's 64 x 32 wave tiles (at M =
-        // 2048 one fp16 block per CU, or two K parts and a combine, measured
-        // slower: 231 against 223 us for the MLP half)
+        // power-of-two scales in the xs area), and the down product on h
+        // written as fp16 / 256 in the operand order (exact for |h| in
+        // [2^-6, 1.6e7]), in mlp_down_parts K parts (2048 x 6144 down at M =
+        // 2048: 71 us in two parts, against 102 us on the exact-operand GEMM
+        // with paired bf16 h).  With the down product's scale or bias rows
+        // not 16-byte aligned, gate/up writes h paired in bf16 with its group
+        // sums for the exact-operand GEMM's down product.
         auto a16 = [](const QMat& q) { return aligned(q.s, 16) && aligned(q.b, 16); };
         if (a16(G) && a16(U)) {
-            const bool down16 = a16(D) && (N / 64) % 8 == 0 &&
-                                ((M + 127) / 128) * ((K + 255) / 256) >= 2 * (int64_t)num_cus();
+            const int parts = a16(D) ? mlp_down_parts(M, K, N) : 0;
+            const bool down16 = parts > 0;
             if (launch_pair_rows16(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
             Gemm16Args gu{w.xp, w.xs, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, down16 ? nullptr : w.hs, 0.0f,
@@ -856,7 +882,7 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
             if (down16) {
                 Gemm16Args dn{w.hp, nullptr, (int)M, (int)K, (int)N, D, QMat{nullptr, nullptr, nullptr}, y, x,
-                              nullptr, 256.0f, 0.0f};
+                              nullptr, 256.0f, 0.0f, parts, w.kpart};
                 if (launch_q4_gemm16(dn, GEMM_RESIDUAL, st))
                     return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
                 return launch_status(what);

@@ -223,7 +223,9 @@ def test_noalloc_lm_head_host_validation(mq4):
 def test_mlp_residual_workspace_and_validation(mq4):
     """mq4_mlp_workspace_size: h [M, N] bf16, plus for 5-32 rows the two fp32
     K parts of the down product [2, M, K], and from 33 rows on the paired x
-    [M, K] and the group sums of x and h, each section 256-byte aligned; the
+    [M, K], the group sums of x and h and the fp16-weight down product's
+    fp32 K parts [S, M, K] (S of 1, 2, 4 with ceil(M / 128) ceil(K / 256) S
+    <= 256 CUs; no section for S = 1), each section 256-byte aligned; the
     entry rejects a missing, small or misaligned workspace (and bad shapes)
     before enqueueing anything."""
     L = mq4.lib()
@@ -234,8 +236,18 @@ def test_mlp_residual_workspace_and_validation(mq4):
     assert L.mq4_mlp_workspace_size(32, 2048, 6144) == up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
     M, K, N = 2048, 2048, 6144
     # from 33 rows: h, the paired (or fp16) operand, its group sums (or row
-    # scales) and h's group sums
-    assert L.mq4_mlp_workspace_size(M, K, N) == up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) + up(M * N // 64 * 4)
+    # scales), h's group sums and (M = 2048: 16 x 8 tiles) two K parts
+    assert L.mq4_mlp_workspace_size(M, K, N) == (up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) +
+                                                 up(M * N // 64 * 4) + up(2 * M * K * 4))
+    # 8192 rows (512 tiles): one part, no section
+    M8 = 8192
+    assert L.mq4_mlp_workspace_size(M8, K, N) == (up(M8 * N * 2) + up(M8 * K * 2) + up(M8 * K // 64 * 4) +
+                                                  up(M8 * N // 64 * 4))
+    # the size for M rows covers every smaller row count, also where the
+    # K-part count drops (1024 rows: four parts)
+    big = L.mq4_mlp_workspace_size(3000, K, N)
+    assert all(L.mq4_mlp_workspace_size(m, K, N) <= big for m in (33, 1024, 1025, 2048, 2049, 3000))
+    assert L.mq4_mlp_workspace_size(1024, K, N) >= up(4 * 1024 * K * 4)
     # the size for M rows covers every call of at most M rows (the paired
     # GEMM regime from 33 rows needs less per row than the two fp32 K parts of
     # 5-32 rows, so the size is the largest over the regimes up to M)
