@@ -175,8 +175,13 @@ int mq4_rmsnorm_gate_up_silu(const uint16_t* x, int64_t M, int64_t K,
  * normalized operand and bf16 h; fp32 sums in another order, so not always
  * bit for bit).  From M = 33 rows on (K and N multiples of 512, scale and
  * bias rows 4-byte aligned) it runs the MFMA GEMM on activations stored in
- * the matrix cores' operand order with their group sums: a pre-pass writes
- * the normalized x so, the SwiGLU epilogue writes h so.  From 5 to 32 rows
+ * the matrix cores' operand order: a pre-pass writes the normalized x so, the
+ * SwiGLU epilogue writes h so.  With every scale and bias row 16-byte
+ * aligned the products use fp16 weights (fp16(s q + b), about 2e-6 of the
+ * output rms from the exact product) on an fp16 copy of the operands, and
+ * the down product runs in 1, 2 or 4 K parts whose fp32 sums go to the
+ * workspace and are added in order with the residual; otherwise the exact
+ * bf16 operands with their group sums.  From 5 to 32 rows
  * (with 64 < N / 64 <= 96) the down product runs as two halves of K per
  * 16-row tile on different workgroups.  Their fp32 sums go to the workspace
  * and a combine pass adds them with the residual, bit for bit what
