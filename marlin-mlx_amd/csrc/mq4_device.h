@@ -165,16 +165,42 @@ __device__ __forceinline__ bool sigmoid_bf16_fast(float g, float& s) {
     const float d = 1.0f + e;
     float r = __builtin_amdgcn_rcpf(d);
     r = __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
+    // low 16 bits outside [0x8000 - SIG_MARGIN, 0x8000 + SIG_MARGIN]: one
+    // unsigned compare of the wrapped offset
     const uint32_t lo = __builtin_bit_cast(uint32_t, r) & 0xffffu;
-    const uint32_t dist = lo > 0x8000u ? lo - 0x8000u : 0x8000u - lo;
     s = round_bf16(r);
-    return __builtin_fabsf(g) < 64.0f && dist > SIG_MARGIN;
+    return __builtin_fabsf(g) < 64.0f && lo - (0x8000u - SIG_MARGIN) > 2u * SIG_MARGIN;
 }
 __device__ __forceinline__ float sigmoid_bf16(float g) {
 #pragma clang fp contract(off)
     float s;
     if (!sigmoid_bf16_fast(g, s)) s = round_bf16(1.0f / (1.0f + expf(-g)));
     return s;
+}
+
+// swiglu_bf16 of N (gate, up) pairs, the same bits: the fast sigmoid of all
+// of them first, then the exact formula for those it did not decide, in one
+// branch for the batch (a branch per value splits the batch's exp and rcp
+// chains into regions the compiler cannot interleave).
+template <int N>
+__device__ __forceinline__ void swiglu_bf16_batch(const float (&g_acc)[N], const float (&u_acc)[N],
+                                                  uint32_t (&out)[N]) {
+#pragma clang fp contract(off)
+    static_assert(N <= 32, "one mask word");
+    float g[N], s[N];
+    uint32_t need = 0;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+        g[e] = round_bf16(g_acc[e]);
+        if (!sigmoid_bf16_fast(g[e], s[e])) need |= 1u << e;
+    }
+    if (need) {
+#pragma unroll
+        for (int e = 0; e < N; ++e)
+            if (need & (1u << e)) s[e] = round_bf16(1.0f / (1.0f + expf(-g[e])));
+    }
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = f32_to_bf16(round_bf16(s[e] * g[e]) * round_bf16(u_acc[e]));
 }
 
 // swiglu_bf16 with sigmoid_bf16: the same bits.

@@ -374,6 +374,17 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
         if (row >= M) return;
         const float sc = (p.xscale ? p.xscale[row] : 1.0f) * ascale;
         const int64_t rowo = (int64_t)row * N;
+        // SwiGLU of the lane's 16 (gate, up) pairs of this tile row
+        uint32_t hv[16];
+        if (EPI == GEMM_SWIGLU) {
+            float ga[16], ua[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                ga[e] = acc[i][0][e] * sc;
+                ua[e] = acc[i][1][e] * sc;
+            }
+            swiglu_bf16_batch<16>(ga, ua, hv);
+        }
 #pragma unroll
         for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
 #pragma unroll
@@ -386,7 +397,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                     uint32_t o[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const uint32_t v = swiglu_bf16_fast(acc[i][0][eg * 4 + q] * sc, acc[i][1][eg * 4 + q] * sc);
+                        const uint32_t v = hv[eg * 4 + q];
                         o[q] = v;
                         if (paired_out) tile[(rl - rbase) * TS + (cl & ~7) + perm8(h * 4 + q)] = (uint16_t)v;
                         if (f16_out) {
