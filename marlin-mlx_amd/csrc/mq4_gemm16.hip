@@ -505,8 +505,11 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
 // largest |x (1 + w)| (|x| without the norm); pass 2 writes bf16(x r (1 + w))
 // (or x), scaled by 2^-e and converted to fp16, in the pair order, and
 // xscale[m] = 2^e.  e is the smallest such that the scaled row stays below
-// 2^15 (0 for every normalized row whose values stay below 2^15).
-template <bool NORM>
+// 2^15 (0 for every normalized row whose values stay below 2^15).  With CAP >
+// 0 (K <= 512 CAP) a lane keeps its chunks of x and of the norm weight in
+// registers between the passes (all loads issued first), so the row is read
+// once; the sums keep the chunk order of the reloading form (CAP = 0).
+template <bool NORM, int CAP>
 __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                           const uint16_t* __restrict__ nw, float eps,
                                                           uint16_t* __restrict__ xp, float* __restrict__ xscale) {
@@ -516,13 +519,23 @@ __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __rest
     if (m >= M) return;                                  // whole waves
     const int CH = K / 8;
     const uint4* src = reinterpret_cast<const uint4*>(x + (int64_t)m * K);
+    const uint4* nw4 = reinterpret_cast<const uint4*>(nw);
     uint4* dst = reinterpret_cast<uint4*>(xp + (int64_t)m * K);
+    constexpr int NC = CAP > 0 ? CAP : 1;
+    uint4 xc[NC], wc[NC];
+    if (CAP > 0) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + 64 * i;
+            if (c < CH) {
+                xc[i] = src[c];
+                wc[i] = NORM ? nw4[c] : make_uint4(0, 0, 0, 0);
+            }
+        }
+    }
     float ss = 0.0f, big = 0.0f;
-    for (int c = lane; c < CH; c += 64) {
-        const uint4 v = src[c];
+    auto scan = [&](const uint4& v, const uint4& wv) {
         const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-        uint4 wv = make_uint4(0, 0, 0, 0);
-        if (NORM) wv = reinterpret_cast<const uint4*>(nw)[c];
         const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -532,6 +545,13 @@ __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __rest
             const float f1 = NORM ? 1.0f + bf16_to_f32(ww[q] >> 16) : 1.0f;
             big = fmaxf(big, fmaxf(fabsf(a0 * f0), fabsf(a1 * f1)));
         }
+    };
+    if (CAP > 0) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i)
+            if (lane + 64 * i < CH) scan(xc[i], wc[i]);
+    } else {
+        for (int c = lane; c < CH; c += 64) scan(src[c], NORM ? nw4[c] : make_uint4(0, 0, 0, 0));
     }
     float r = 1.0f;
     if (NORM) r = rms_inv(wave_sum(ss), K, eps);
@@ -543,13 +563,10 @@ __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __rest
     while (!(big * 1.01f < 32768.0f * __builtin_ldexpf(1.0f, e)) && e < 200) ++e;
     const float down = __builtin_ldexpf(1.0f, -e);
     if (lane == 0) xscale[m] = __builtin_ldexpf(1.0f, e);
-    for (int c = lane; c < CH; c += 64) {
-        uint4 v = src[c];
-        if (NORM) {
-            const uint4 w = reinterpret_cast<const uint4*>(nw)[c];
+    auto emit = [&](int c, uint4 v, const uint4& w) {
+        if (NORM)
             v = make_uint4(norm_word(v.x, w.x, r), norm_word(v.y, w.y, r), norm_word(v.z, w.z, r),
                            norm_word(v.w, w.w, r));
-        }
         uint32_t pr[4];
         pair_chunk(v, pr, 0.0f);
         uint32_t o[4];
@@ -560,6 +577,15 @@ __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __rest
             o[q] = __builtin_bit_cast(uint32_t, hv);
         }
         dst[c] = make_uint4(o[0], o[1], o[2], o[3]);
+    };
+    if (CAP > 0) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + 64 * i;
+            if (c < CH) emit(c, xc[i], wc[i]);
+        }
+    } else {
+        for (int c = lane; c < CH; c += 64) emit(c, src[c], NORM ? nw4[c] : make_uint4(0, 0, 0, 0));
     }
 }
 
@@ -595,12 +621,20 @@ int launch_pair_rows16(const uint16_t* x, int M, int K, const uint16_t* norm_w, 
                        float* xscale, hipStream_t st) {
     if (M < 1 || K % 512 != 0) return -1;
     const unsigned blocks = (unsigned)((M + 3) / 4);
-    if (norm_w)
-        hipLaunchKernelGGL(g16::pair_rows16_kernel<true>, dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps, xp,
-                           xscale);
+    // rows of at most 4 chunks per lane (K <= 2048) read once
+    const bool cached = K / 512 <= 4;
+    if (norm_w && cached)
+        hipLaunchKernelGGL((g16::pair_rows16_kernel<true, 4>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
+                           xp, xscale);
+    else if (norm_w)
+        hipLaunchKernelGGL((g16::pair_rows16_kernel<true, 0>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
+                           xp, xscale);
+    else if (cached)
+        hipLaunchKernelGGL((g16::pair_rows16_kernel<false, 4>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
+                           xp, xscale);
     else
-        hipLaunchKernelGGL(g16::pair_rows16_kernel<false>, dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps, xp,
-                           xscale);
+        hipLaunchKernelGGL((g16::pair_rows16_kernel<false, 0>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
+                           xp, xscale);
     return 0;
 }
 
