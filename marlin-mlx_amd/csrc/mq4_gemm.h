@@ -57,7 +57,7 @@ struct Gemm16Args {
     float* ysum;
     float ascale;            // a power of two, or 0 (1)
     float yscale;            // GEMM_SWIGLU: fp16 output scale, or 0 (bf16 output)
-    // GEMM_RESIDUAL in ksplit > 1 K parts (K / 64 a multiple of 8 ksplit):
+    // GEMM_RESIDUAL in 1 < ksplit <= 4 K parts (K / 64 a multiple of 8 ksplit):
     // part[k][M][N] fp32 (16-byte aligned, N % 4 == 0), then a second kernel
     // adds the parts in order and the residual (res and y 8-byte aligned)
     int ksplit;

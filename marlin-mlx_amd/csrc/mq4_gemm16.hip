@@ -591,22 +591,29 @@ __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __rest
 
 // y = bf16(res + round_bf16(part[0] + part[1] + ... + part[S - 1])), the
 // parts added in order: 4 elements per thread (MN % 4 == 0, 16-byte aligned
-// parts, 8-byte aligned res and y).
+// parts, 8-byte aligned res and y), S <= 4.
 __global__ __launch_bounds__(256) void kpart_residual_kernel(const float* __restrict__ part, int S, int64_t MN,
                                                              const uint16_t* __restrict__ res,
                                                              uint16_t* __restrict__ y) {
 #pragma clang fp contract(off)
     const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (e >= MN) return;
-    float4 sum = *reinterpret_cast<const float4*>(part + e);
-    for (int k = 1; k < S; ++k) {
-        const float4 v = *reinterpret_cast<const float4*>(part + (int64_t)k * MN + e);
-        sum.x += v.x;
-        sum.y += v.y;
-        sum.z += v.z;
-        sum.w += v.w;
-    }
+    // every load issued before the first add (S <= 4 parts)
+    float4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (k < S) v[k] = *reinterpret_cast<const float4*>(part + (int64_t)k * MN + e);
     const uint2 r = *reinterpret_cast<const uint2*>(res + e);
+    float4 sum = v[0];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+        if (k < S) {
+            sum.x += v[k].x;
+            sum.y += v[k].y;
+            sum.z += v[k].z;
+            sum.w += v[k].w;
+        }
+    }
     const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
     const uint32_t rv[4] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16};
     uint32_t o[4];
@@ -646,11 +653,11 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
     if (!fits32 || a.K % 512 != 0 || a.M < 1 || a.N < 1 || !a16(a.A) || (epi == GEMM_SWIGLU && !a16(a.B))) return -1;
     if (a.ysum && (epi != GEMM_SWIGLU || a.yscale != 0.0f || a.N % 128 != 0)) return -1;
     if (a.yscale != 0.0f && (epi != GEMM_SWIGLU || a.N % 8 != 0)) return -1;
-    // K parts: GEMM_RESIDUAL only, whole 8-group scale slots per part, fp32
-    // parts [ksplit][M][N] (16-byte aligned, N % 4 == 0) combined by a second
-    // kernel
+    // K parts: GEMM_RESIDUAL only, at most 4, whole 8-group scale slots per
+    // part, fp32 parts [ksplit][M][N] (16-byte aligned, N % 4 == 0) combined
+    // by a second kernel
     const int S = a.ksplit > 1 ? a.ksplit : 1;
-    if (S > 1 && (epi != GEMM_RESIDUAL || (a.K / 64) % (8 * S) != 0 || !a.part ||
+    if (S > 1 && (epi != GEMM_RESIDUAL || S > 4 || (a.K / 64) % (8 * S) != 0 || !a.part ||
                   reinterpret_cast<uintptr_t>(a.part) % 16 != 0 || a.N % 4 != 0 || !aligned(a.res, 8) ||
                   !aligned(a.y, 8)))
         return -1;
