@@ -41,8 +41,8 @@ int launch_q4_gemm(const GemmArgs& a, int epi, bool norm, hipStream_t st);
 // The fp16-weight GEMM (mq4_gemm16.hip): x holds fp16 activations in the
 // operand order of launch_pair_rows16, row m scaled by 1 / (xscale[m] *
 // ascale) (xscale null: 1; ascale 0: 1), and the product of row m is
-// multiplied back by xscale[m] * ascale (powers of two).  Epilogues as
-// GemmArgs, plus:
+// multiplied back by xscale[m] * ascale (powers of two).  Epilogues
+// GEMM_RESIDUAL and GEMM_SWIGLU as GemmArgs, plus:
 //  * GEMM_SWIGLU with yscale != 0: y = fp16(h * yscale) in the operand order
 //    (h the bf16 SwiGLU value; saturated at +-65504), no ysum; with
 //    yscale == 0 and ysum: the bf16 paired h and its group sums (N % 128 ==
@@ -64,8 +64,10 @@ struct Gemm16Args {
     float* part;
 };
 
-// Enqueue the fp16-weight GEMM; 0, or -1 for shapes it does not take (K % 512
-// != 0, scales or biases not 16-byte aligned, byte offsets past 32 bits).
+// Enqueue the fp16-weight GEMM (GEMM_SWIGLU or GEMM_RESIDUAL, the products of
+// mq4_mlp_residual); 0, or -1 for another epilogue or shapes it does not take
+// (K % 512 != 0, scales or biases not 16-byte aligned, byte offsets past 32
+// bits).
 int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st);
 
 // xp = fp16(x / xscale[m]) (norm_w null) or fp16(bf16(x * rsqrt(mean(x^2) +

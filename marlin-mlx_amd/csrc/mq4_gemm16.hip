@@ -142,6 +142,7 @@ __device__ __forceinline__ void mfma_result_pad() {
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
 #pragma clang fp contract(off)
+    static_assert(EPI == GEMM_SWIGLU || EPI == GEMM_RESIDUAL, "the epilogues of mq4_mlp_residual");
     constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
     constexpr int BN = BNW / NMAT;                       // output columns per block
     __shared__ Stage st0, st1;
@@ -363,10 +364,11 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     constexpr int TS = BN + 8;                                     // bf16 per epilogue tile row
     uint16_t* tile = reinterpret_cast<uint16_t*>(&st0);          // [64][TS] bf16
     static_assert(64 * (BNW / 2 + 8) * 2 <= (int)sizeof(Stage), "epilogue tile");
-    // whole-run vector stores: N % 4 == 0 and 8-byte (fp32: 16-byte) aligned y and res
+    // whole-run vector stores: N % 4 == 0 and 8-byte aligned y and res
+    // (16-byte aligned fp32 parts)
     const bool vec = N % 4 == 0 &&
                      (S > 1 ? reinterpret_cast<uintptr_t>(p.part) % 16 == 0
-                            : reinterpret_cast<uintptr_t>(p.y) % (EPI == GEMM_STORE_F32 ? 16 : 8) == 0 &&
+                            : reinterpret_cast<uintptr_t>(p.y) % 8 == 0 &&
                                   (EPI != GEMM_RESIDUAL || reinterpret_cast<uintptr_t>(p.res) % 8 == 0));
     const float ascale = p.ascale != 0.0f ? p.ascale : 1.0f;
     auto emit = [&](int i, int rbase) {
@@ -419,8 +421,8 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                 float v[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) v[q] = acc[i][j][eg * 4 + q] * sc;
-                if (EPI == GEMM_STORE_F32 || S > 1) {
-                    float* y = (S > 1 ? p.part + (int64_t)kpart * M * N : reinterpret_cast<float*>(p.y)) + rowo + cb;
+                if (S > 1) {
+                    float* y = p.part + (int64_t)kpart * M * N + rowo + cb;
                     if (whole) {
                         *reinterpret_cast<float4*>(y) = make_float4(v[0], v[1], v[2], v[3]);
                     } else {
@@ -432,22 +434,17 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                 }
                 uint32_t o[4];
                 uint16_t* y = reinterpret_cast<uint16_t*>(p.y) + rowo + cb;
-                if (EPI == GEMM_STORE) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) o[q] = f32_to_bf16(v[q]);
+                const uint16_t* r = p.res + rowo + cb;
+                uint32_t rv[4];
+                if (whole) {
+                    const uint2 t = *reinterpret_cast<const uint2*>(r);
+                    rv[0] = t.x & 0xffffu; rv[1] = t.x >> 16; rv[2] = t.y & 0xffffu; rv[3] = t.y >> 16;
                 } else {
-                    const uint16_t* r = p.res + rowo + cb;
-                    uint32_t rv[4];
-                    if (whole) {
-                        const uint2 t = *reinterpret_cast<const uint2*>(r);
-                        rv[0] = t.x & 0xffffu; rv[1] = t.x >> 16; rv[2] = t.y & 0xffffu; rv[3] = t.y >> 16;
-                    } else {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) rv[q] = cb + q < N ? r[q] : 0u;
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) o[q] = f32_to_bf16(bf16_to_f32(rv[q]) + round_bf16(v[q]));
+                    for (int q = 0; q < 4; ++q) rv[q] = cb + q < N ? r[q] : 0u;
                 }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[q] = f32_to_bf16(bf16_to_f32(rv[q]) + round_bf16(v[q]));
                 if (whole) {
                     *reinterpret_cast<uint2*>(y) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
                 } else {
@@ -664,12 +661,6 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
     const int BN = epi == GEMM_SWIGLU ? g16::BNW / 2 : g16::BNW;
     const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + g16::TBM - 1) / g16::TBM) * S);
     switch (epi) {
-        case GEMM_STORE:
-            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_STORE>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
-            return 0;
-        case GEMM_STORE_F32:
-            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_STORE_F32>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
-            return 0;
         case GEMM_RESIDUAL: {
             hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_RESIDUAL>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
             if (S > 1) {
