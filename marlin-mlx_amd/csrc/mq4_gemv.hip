@@ -872,7 +872,10 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
         // sums for the exact-operand GEMM's down product.
         auto a16 = [](const QMat& q) { return aligned(q.s, 16) && aligned(q.b, 16); };
         if (a16(G) && a16(U)) {
-            const int parts = a16(D) ? mlp_down_parts(M, K, N) : 0;
+            // K parts need an 8-byte aligned y (one part stores any 2-byte
+            // aligned y element by element)
+            int parts = a16(D) ? mlp_down_parts(M, K, N) : 0;
+            if (parts > 1 && !aligned(y, 8)) parts = 1;
             const bool down16 = parts > 0;
             if (launch_pair_rows16(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);

@@ -258,6 +258,37 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     assert rel_o <= TOL
 
 
+@pytest.mark.gpu
+def test_mlp_residual_unaligned_output(mq4, O, dev):
+    """The one-call MLP at 200 rows (fp16-weight GEMM; four K parts of the
+    down product for an 8-byte aligned y) into a y that is only 2-byte
+    aligned, which the entry accepts: the down product then runs as one part
+    and stores element by element.  Same result up to the parts' fp32
+    summation order: >= 99% of the bits identical, rms of the difference
+    <= 1e-3 of the MLP output's rms."""
+    import torch
+    M, K, N = 200, 2048, 6144
+    print(f"mlp_residual unaligned y M={M}", flush=True)
+    ws = [make(mq4, O, *((N, K) if p < 2 else (K, N)), 1300 + p, dev) for p in range(3)]
+    w = mq4.MLPWeights(*[mq4.QuantizedTensor(*d) for d, _ in ws])
+    x = mq4.fill_normal_bf16((M, K), mq4.STREAM_PREFILL + 2, 0.0, 1.0, device=dev)
+    nw = mq4.fill_normal_bf16((K,), mq4.stream_id_layer_norm(2), 0.1, 0.02, device=dev)
+    ref = mq4.mlp_residual(x, w, nw, 1e-6)
+    buf = torch.zeros(M * K + 1, dtype=torch.bfloat16, device=dev)
+    yo = buf[1:].view(M, K)                                # 2-byte aligned, not 8
+    assert yo.data_ptr() % 8 != 0
+    mq4.mlp_residual(x, w, nw, 1e-6, out=yo)
+    torch.cuda.synchronize()
+    got, want, xh = to_host_u16(yo), to_host_u16(ref), to_host_u16(x)
+    same = float(np.mean(got == want))
+    xf = O.bf16_to_f32(xh).astype(np.float64)
+    d = (O.bf16_to_f32(got) - O.bf16_to_f32(want)).astype(np.float64)
+    ms = O.bf16_to_f32(want).astype(np.float64) - xf
+    rel = float(np.sqrt(np.mean(d * d) / np.mean(ms * ms)))
+    print(f"identical {same:.5f}, rms(diff)/rms(mlp) {rel:.2e}")
+    assert same >= 0.99 and rel <= 1e-3
+
+
 @pytest.mark.parametrize("M", [16, 32, 200])
 def test_mlp_residual_split_graph_replay(mq4, O, dev, M):
     """The one-call MLP with its down product in K parts plus a combine,
