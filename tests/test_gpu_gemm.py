@@ -259,6 +259,61 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M", [200, 1960])
+def test_mlp_residual_paired_down(mq4, O, dev, M):
+    """The one-call MLP with the down matrix's scales and biases 4-byte but not
+    16-byte aligned: gate/up on the fp16-weight GEMM writes h paired in bf16
+    (pair order through the per-chunk column permutation) with its group sums
+    from the LDS tile, and the down product runs on the exact-operand GEMM.
+    Against the separate entries: >= 95% of the bits identical, rms of the
+    difference <= 1e-2 of the MLP output's rms; against the oracle chain on
+    sampled rows: rms(err) <= 1e-2 of that rms."""
+    import torch
+    K, N = 2048, 6144
+    print(f"mlp_residual paired down M={M}", flush=True)
+    ws = [make(mq4, O, *((N, K) if p < 2 else (K, N)), 1400 + p, dev) for p in range(3)]
+    (gd, _), (ud, _), (dd, _) = ws
+    keep = []
+
+    def shifted(t):                                       # the same values 4 bytes past a 16-byte boundary
+        buf = torch.empty(t.numel() + 2, dtype=t.dtype, device=dev)
+        v = buf[2:].view(t.shape)
+        v.copy_(t)
+        keep.append(buf)
+        return v
+
+    ds, db = shifted(dd[1]), shifted(dd[2])
+    assert ds.data_ptr() % 16 != 0 and ds.data_ptr() % 4 == 0 and db.data_ptr() % 16 != 0
+    w = mq4.MLPWeights(mq4.QuantizedTensor(*gd), mq4.QuantizedTensor(*ud), mq4.QuantizedTensor(dd[0], ds, db))
+    x = mq4.fill_normal_bf16((M, K), mq4.STREAM_PREFILL + 3, 0.0, 1.0, device=dev)
+    nw = mq4.fill_normal_bf16((K,), mq4.stream_id_layer_norm(3), 0.1, 0.02, device=dev)
+    y = mq4.mlp_residual(x, w, nw, 1e-6)
+    h = mq4.mlp_gate_up_silu(x, w.gate_proj, w.up_proj, norm_weight=nw, eps=1e-6)
+    ys = mq4.qmatmul_residual(h, w.down_proj, x)
+    torch.cuda.synchronize()
+    got, sep, xh = to_host_u16(y), to_host_u16(ys), to_host_u16(x)
+    same = float(np.mean(got == sep))
+    xf = O.bf16_to_f32(xh).astype(np.float64)
+    dm = (O.bf16_to_f32(got) - O.bf16_to_f32(sep)).astype(np.float64)
+    ms = O.bf16_to_f32(sep).astype(np.float64) - xf
+    rel = float(np.sqrt(np.mean(dm * dm) / np.mean(ms * ms)))
+    print(f"vs separate entries: identical {same:.5f}, rms(diff)/rms(mlp) {rel:.2e}")
+    assert same >= 0.95 and rel <= TOL
+    rows = sampled_rows(M)
+    rows = rows[(rows >= 0) & (rows < M)]
+    xs = xh[rows]
+    n = O.rmsnorm_1pw(xs, to_host_u16(nw), 1e-6)
+    (_, gh), (_, uh), (_, dh) = ws
+    _, _, _, yb = O.mlp_forward(n, gh, uh, dh)
+    ref = O.add_bf16(xs, yb)
+    err = (O.bf16_to_f32(got[rows]) - O.bf16_to_f32(ref)).astype(np.float64)
+    mo = O.bf16_to_f32(yb).astype(np.float64)
+    rel_o = float(np.sqrt(np.mean(err * err) / np.mean(mo * mo)))
+    print(f"vs oracle chain: rms(err)/rms(mlp) {rel_o:.2e}")
+    assert rel_o <= TOL
+
+
+@pytest.mark.gpu
 def test_mlp_residual_unaligned_output(mq4, O, dev):
     """The one-call MLP at 200 rows (fp16-weight GEMM; four K parts of the
     down product for an 8-byte aligned y) into a y that is only 2-byte
