@@ -259,18 +259,19 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [200, 1960])
-def test_mlp_residual_paired_down(mq4, O, dev, M):
-    """The one-call MLP with the down matrix's scales and biases 4-byte but not
-    16-byte aligned: gate/up on the fp16-weight GEMM writes h paired in bf16
-    (pair order through the per-chunk column permutation) with its group sums
-    from the LDS tile, and the down product runs on the exact-operand GEMM.
-    Against the separate entries: >= 95% of the bits identical, rms of the
-    difference <= 1e-2 of the MLP output's rms; against the oracle chain on
-    sampled rows: rms(err) <= 1e-2 of that rms."""
+@pytest.mark.parametrize("M,shift", [(200, "down"), (1960, "down"), (200, "gate")])
+def test_mlp_residual_paired_down(mq4, O, dev, M, shift):
+    """The one-call MLP with one matrix's scales and biases 4-byte but not
+    16-byte aligned.  down: gate/up on the fp16-weight GEMM writes h paired
+    in bf16 (pair order through the per-chunk column permutation) with its
+    group sums from the LDS tile, and the down product runs on the
+    exact-operand GEMM.  gate: both products on the exact-operand GEMM with
+    paired operands.  Against the separate entries: >= 95% of the bits
+    identical, rms of the difference <= 1e-2 of the MLP output's rms; against
+    the oracle chain on sampled rows: rms(err) <= 1e-2 of that rms."""
     import torch
     K, N = 2048, 6144
-    print(f"mlp_residual paired down M={M}", flush=True)
+    print(f"mlp_residual shifted {shift} scales M={M}", flush=True)
     ws = [make(mq4, O, *((N, K) if p < 2 else (K, N)), 1400 + p, dev) for p in range(3)]
     (gd, _), (ud, _), (dd, _) = ws
     keep = []
@@ -282,9 +283,12 @@ def test_mlp_residual_paired_down(mq4, O, dev, M):
         keep.append(buf)
         return v
 
-    ds, db = shifted(dd[1]), shifted(dd[2])
-    assert ds.data_ptr() % 16 != 0 and ds.data_ptr() % 4 == 0 and db.data_ptr() % 16 != 0
-    w = mq4.MLPWeights(mq4.QuantizedTensor(*gd), mq4.QuantizedTensor(*ud), mq4.QuantizedTensor(dd[0], ds, db))
+    sel = dd if shift == "down" else gd
+    ss, sb = shifted(sel[1]), shifted(sel[2])
+    assert ss.data_ptr() % 16 != 0 and ss.data_ptr() % 4 == 0 and sb.data_ptr() % 16 != 0
+    q = mq4.QuantizedTensor(sel[0], ss, sb)
+    w = (mq4.MLPWeights(mq4.QuantizedTensor(*gd), mq4.QuantizedTensor(*ud), q) if shift == "down" else
+         mq4.MLPWeights(q, mq4.QuantizedTensor(*ud), mq4.QuantizedTensor(*dd)))
     x = mq4.fill_normal_bf16((M, K), mq4.STREAM_PREFILL + 3, 0.0, 1.0, device=dev)
     nw = mq4.fill_normal_bf16((K,), mq4.stream_id_layer_norm(3), 0.1, 0.02, device=dev)
     y = mq4.mlp_residual(x, w, nw, 1e-6)
