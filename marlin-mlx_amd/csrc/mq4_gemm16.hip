@@ -41,8 +41,10 @@
 //  * Per 64-k group, the 128 x 64 activations (16 KB, each row's eight
 //    16-byte chunks XOR-swizzled by (row / 2) % 8: the 16 lanes of a
 //    ds_read_b128 phase, 16 rows at one chunk, cover the 64 banks once) and
-//    the 256 x 32 bytes of packed weights (two lanes per weight column, its
-//    32 contiguous bytes) go to LDS by DMA, two stages, one group ahead;
+//    the 256 x 32 bytes of packed weights (per 32 columns one DMA
+//    instruction, lane l reading k-half l / 32 of column l % 32, so that the
+//    stage holds each k-half's 32 columns in consecutive slots) go to LDS by
+//    DMA, two stages, one group ahead;
 //    the columns' scales and biases follow every eight groups (16 bytes per
 //    column, two slots).  Each step waits for all of its wave's DMA;
 //    barriers carry no memory fence.  (Per-group DMA of the scales, four
@@ -85,7 +87,7 @@ constexpr int SB_I = 2 * BNW / (64 * kNW);// scale/bias DMA instructions per wav
 
 struct Stage {
     uint4 a[TBM * 8];                     // [row][chunk ^ ((row >> 1) & 7)], fp16 pairs
-    uint4 b[2 * BNW];                     // [weight column][k-half]
+    uint4 b[2 * BNW];                     // [32-column block][k-half][column]
 };
 // Scales and biases of 8 groups: [scales | biases][weight column], 16 bytes
 // (groups 8 t .. 8 t + 7) each.
@@ -198,15 +200,17 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
         return n < N ? n : N - 1;
     };
     auto mat_of = [&](int r) -> const QMat& { return (NMAT == 2 && r >= BNW / 2) ? p.B : p.A; };
-    // packed weights: instruction t covers 32 weight columns, two lanes per
-    // column (its group's two 16-byte k-halves, 32 contiguous bytes)
+    // packed weights: instruction t covers 32 weight columns, lane l takes
+    // k-half l / 32 of column l % 32 (its group's 32 bytes as two 16-byte
+    // halves), so the stage holds [32-column block][k-half][column] and the
+    // operand reads of a k-half are 32 consecutive 16-byte slots
     const char* bbase[B_I];
     uint32_t boff[B_I];
 #pragma unroll
     for (int t = 0; t < B_I; ++t) {
-        const int q0 = (wave * B_I + t) * 64, r0 = q0 >> 1;
+        const int r0 = (wave * B_I + t) * 32;
         bbase[t] = reinterpret_cast<const char*>(mat_of(r0).wq) + (int64_t)kpart * GL * 32;
-        boff[t] = (uint32_t)((int64_t)wrow_of(r0 + (lane >> 1)) * (K / 2) + (lane & 1) * 16);
+        boff[t] = (uint32_t)((int64_t)wrow_of(r0 + (lane & 31)) * (K / 2) + (lane >> 5) * 16);
     }
     // scales and biases: 16 bytes (8 groups) of one weight column per lane
     const char* sbbase[SB_I];
@@ -264,7 +268,7 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
         const int sh16 = (g & 1) * 16, dw = (g >> 1) & 3;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            w.bw[j] = st.b[wr[j] * 2 + h];
+            w.bw[j] = st.b[(wr[j] >> 5) * 64 + h * 32 + (wr[j] & 31)];
             const _Float16 s = bf16_to_h((reinterpret_cast<const uint32_t*>(&sbs.v[0][wr[j]])[dw] >> sh16) & 0xffffu);
             const _Float16 b = bf16_to_h((reinterpret_cast<const uint32_t*>(&sbs.v[1][wr[j]])[dw] >> sh16) & 0xffffu);
             w.s2[j] = (h2_t){s, s};
