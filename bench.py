@@ -20,7 +20,7 @@ Output: one JSON line on stdout.  `value` is the step's algorithmic HBM
 bandwidth, Q4 weight bytes per step (795,672,576 B) / step time; inputs are
 resident in HBM before the timed region and the 796 MB weight stream is larger
 than the 256 MB last-level cache, so every step reads the weights from HBM.
-`configs` holds the other BASELINE configurations, each with its own
+`configs` holds the other benchmark configurations, each with its own
 roofline: the single gate GEMV cold and warm (config 1), the 24-layer MLP
 chain (2), lm_head + argmax (3), the prefill GEMM (4), batched decode (5a)
 and the pack of the full weight set (5b).

@@ -1,4 +1,4 @@
-"""Batched decode (M concurrent token rows, BASELINE config 5a) on the model's
+"""Batched decode (M concurrent token rows, bench config 5a) on the model's
 shapes through the C ABI, against the oracle on the same seeded inputs:
 
 * fused gate/up + SwiGLU (6144x2048), with and without the (1 + w) RMSNorm

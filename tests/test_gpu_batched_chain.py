@@ -1,4 +1,4 @@
-"""Batched decode (BASELINE config 5a) end to end: M token rows through the
+"""Batched decode (bench config 5a) end to end: M token rows through the
 benchmark's 24 layers and the 248,320-row lm_head, against the oracle's chain.
 
 Per layer the reference runs the MLP half of src/model/marlin.cpp:141-142

@@ -83,7 +83,7 @@ def test_gemm_qmm_small_against_fp64(mq4, O, dev, M, N, K):
 
 @pytest.mark.parametrize("M", [1960, 2048, 8192])
 def test_gemm_prefill_shapes_sampled_rows(mq4, O, dev, M):
-    """BASELINE prefill: M tokens through gate (6144x2048) and down (2048x6144)."""
+    """Prefill shapes: M tokens through gate (6144x2048) and down (2048x6144)."""
     print(f"prefill M={M}", flush=True)
     rows = np.unique(np.concatenate([np.arange(0, M, max(1, M // 13)), [M - 1, M - 2, 127, 128]]))
     for (N, K, sid) in [(6144, 2048, 1000), (2048, 6144, 1002)]:
