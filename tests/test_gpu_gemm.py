@@ -195,7 +195,8 @@ def test_gemm_epilogues_at_prefill_m(mq4, O, dev):
 
 @pytest.mark.parametrize("M,K,N", [(1960, 2048, 6144), (200, 2048, 6144), (40, 512, 1024), (5, 2048, 6144),
                                    (16, 2048, 6144), (32, 2048, 6144), (24, 2048, 4608), (7, 1024, 5120),
-                                   (23, 2048, 6144), (70, 640, 1280), (4096, 2048, 6144), (8192, 2048, 6144)])
+                                   (23, 2048, 6144), (70, 640, 1280), (4096, 2048, 6144), (8192, 2048, 6144),
+                                   (200, 2048, 1536), (130, 1024, 2048)])
 def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     """mq4_mlp_residual: x + mlp_forward(rms_norm(x)) in one call
     (src/model/marlin.cpp:141-142).  From 33 rows on with K, N multiples of 512
@@ -206,7 +207,10 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     tiles above that: (4096, ...) and (8192, ...) (512 and 1024 blocks of
     128 x 128 on 256 CUs), the prefill bench's M = 8192 figure, run the 64 x 64
     instance, checked on sampled rows that include three of the last 128-row
-    tile (M - 1, M - 2, M - 40); (5, ...),
+    tile (M - 1, M - 2, M - 40); (200, 2048, 1536): 12 gate/up column blocks
+    (not a multiple of 8, the plain block order) and a 24-group down product
+    in one part; (130, 1024, 2048): four down parts of one 8-group scale slot
+    each; (5, ...),
     (16, ...), (32, ...), (23, ...), (24, 2048, 4608) and (7, 1024, 5120)
     take the MFMA GEMV kernels, the down product as two K parts per tile and
     a combine (72 and 80 groups: the second part partly empty), and (70, 640,
