@@ -13,7 +13,9 @@ namespace {
 // sigmoid path decided (no exact fallback), bit 1 = sigmoid_bf16(g) differs
 // from round_bf16(1 / (1 + expf(-g))), bit 2 = swiglu_bf16_fast(g, u)
 // differs from swiglu_bf16(g, u) for one of the u below (bits compared; both
-// NaN counts as equal).
+// NaN counts as equal), bit 3 = swiglu_bf16_batch<16> over g and 15 other
+// bf16 patterns (b + 4099 k, u cycling through the same values) differs
+// from swiglu_bf16 in any of the 16.
 __global__ void sigmoid_check_kernel(uint32_t* status) {
 #pragma clang fp contract(off)
     const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -33,6 +35,20 @@ __global__ void sigmoid_check_kernel(uint32_t* status) {
         const uint32_t a = mq4::swiglu_bf16_fast(g, us[k]), r = mq4::swiglu_bf16(g, us[k]);
         const bool nan_a = (a & 0x7fffu) > 0x7f80u, nan_r = (r & 0x7fffu) > 0x7f80u;
         if (a != r && !(nan_a && nan_r)) st |= 4u;
+    }
+    float ga[16], ua[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        ga[e] = mq4::bf16_to_f32((b + 4099u * (uint32_t)e) & 0xffffu);
+        ua[e] = us[e & 3];
+    }
+    uint32_t hv[16];
+    mq4::swiglu_bf16_batch<16>(ga, ua, hv);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const uint32_t r = mq4::swiglu_bf16(ga[e], ua[e]);
+        const bool nan_a = (hv[e] & 0x7fffu) > 0x7f80u, nan_r = (r & 0x7fffu) > 0x7f80u;
+        if (hv[e] != r && !(nan_a && nan_r)) st |= 8u;
     }
     status[b] = st;
 }
