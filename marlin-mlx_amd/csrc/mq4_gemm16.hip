@@ -3,8 +3,10 @@
 //
 // Same call sites as mq4_gemm.hip: qmatmul (src/model/marlin.cpp:18-25)
 // inside mlp_forward (:31-35) over all S prompt tokens, with the rms_norm in
-// front (:141, :12-16) and the swiglu (:27-29) fused in; used for the gate/up
-// product of mq4_mlp_residual.
+// front (:141, :12-16) and the swiglu (:27-29) fused in; used for both
+// products of mq4_mlp_residual: gate/up with the SwiGLU epilogue, and down
+// with the residual add (:142), whole or in K parts whose fp32 sums
+// kpart_residual_kernel adds in order.
 //
 //   Y[M, N] = X[M, K] . W[N, K]^T,  W[n, k] = s[n, g] * q[n, k] + b[n, g],  g = k / 64
 //
