@@ -377,10 +377,71 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                             : reinterpret_cast<uintptr_t>(p.y) % 8 == 0 &&
                                   (EPI != GEMM_RESIDUAL || reinterpret_cast<uintptr_t>(p.res) % 8 == 0));
     const float ascale = p.ascale != 0.0f ? p.ascale : 1.0f;
+    // The lane's four row scales, loaded together (one wait, not one per
+    // row tile).
+    float scv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + i * 32 + col;
+        scv[i] = (p.xscale && row < M ? p.xscale[row] : 1.0f) * ascale;
+    }
+    // One-part residual epilogue: the residual runs of all four row tiles
+    // are loaded before the first is written (one wait, not one per run).
+    // In place (res == y) every element is read and written by the same
+    // lane, the read first.
+    constexpr bool kResRuns = EPI == GEMM_RESIDUAL;
+    const bool res_runs = kResRuns && S == 1;
+    uint2 resv[4][8];
+    const bool res_whole = vec && n0 + BN <= N;          // every run of the block: one 8-byte load
+    auto load_res = [&](int i, uint2 (&rv)[8]) {
+        const int row = m0 + i * 32 + col;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int eg = 0; eg < 4; ++eg) {
+                const int cb = n0 + wave * 64 + j * 32 + eg * 8 + h * 4;
+                uint2 t = make_uint2(0u, 0u);
+                if (row < M && cb < N) {
+                    const uint16_t* r = p.res + (int64_t)row * N + cb;
+                    if (vec && cb + 3 < N) {
+                        t = *reinterpret_cast<const uint2*>(r);
+                    } else {
+                        uint32_t e[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) e[q] = cb + q < N ? r[q] : 0u;
+                        t = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+                    }
+                }
+                rv[j * 4 + eg] = t;
+            }
+    };
+    if (kResRuns && res_runs) {
+        if (res_whole) {
+            // rows past M read row M - 1 (never stored): no branch between
+            // the loads
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + i * 32 + col;
+                const uint16_t* r = p.res + (int64_t)(row < M ? row : M - 1) * N + n0 + wave * 64 + h * 4;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int eg = 0; eg < 4; ++eg)
+                        resv[i][j * 4 + eg] = *reinterpret_cast<const uint2*>(r + j * 32 + eg * 8);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) load_res(i, resv[i]);
+        }
+    }
+    // One wait for the row scales and residual runs, before the first branch
+    // of the epilogue: past it the compiler's waits at branch joins would
+    // count this tile's stores and drain them.
+    wait_vmcnt<0>();
     auto emit = [&](int i, int rbase) {
         const int rl = i * 32 + col, row = m0 + rl;
         if (row >= M) return;
-        const float sc = (p.xscale ? p.xscale[row] : 1.0f) * ascale;
+        const float sc = scv[i];
         const int64_t rowo = (int64_t)row * N;
         // SwiGLU of the lane's 16 (gate, up) pairs of this tile row
         uint32_t hv[16];
@@ -440,15 +501,8 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                 }
                 uint32_t o[4];
                 uint16_t* y = reinterpret_cast<uint16_t*>(p.y) + rowo + cb;
-                const uint16_t* r = p.res + rowo + cb;
-                uint32_t rv[4];
-                if (whole) {
-                    const uint2 t = *reinterpret_cast<const uint2*>(r);
-                    rv[0] = t.x & 0xffffu; rv[1] = t.x >> 16; rv[2] = t.y & 0xffffu; rv[3] = t.y >> 16;
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) rv[q] = cb + q < N ? r[q] : 0u;
-                }
+                const uint2 t = resv[i][j * 4 + eg];
+                const uint32_t rv[4] = {t.x & 0xffffu, t.x >> 16, t.y & 0xffffu, t.y >> 16};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) o[q] = f32_to_bf16(bf16_to_f32(rv[q]) + round_bf16(v[q]));
                 if (whole) {
