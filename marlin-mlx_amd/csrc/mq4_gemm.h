@@ -62,6 +62,9 @@ struct Gemm16Args {
     // adds the parts in order and the residual (res and y 8-byte aligned)
     int ksplit;
     float* part;
+    // GEMM_RESIDUAL: nonzero for blocks of 128 weight columns (one 32-column
+    // MFMA tile per wave, three blocks per CU) instead of 256; the same bits
+    int narrow;
 };
 
 // Enqueue the fp16-weight GEMM (GEMM_SWIGLU or GEMM_RESIDUAL, the products of

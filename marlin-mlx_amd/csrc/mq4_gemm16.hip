@@ -81,22 +81,30 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kNW = 4;                    // waves per block
 constexpr int kThreads = 64 * kNW;
 constexpr int TBM = 128;                  // rows per block
-constexpr int BNW = 64 * kNW;             // weight columns per block
 constexpr int A_I = TBM * 8 / (64 * kNW); // activation DMA instructions per wave and group (4)
-constexpr int B_TOT = 2 * BNW / 64;       // weight DMA instructions per block and group (8)
-constexpr int B_I = B_TOT / kNW;          // per wave (2)
-constexpr int SB_I = 2 * BNW / (64 * kNW);// scale/bias DMA instructions per wave and 8 groups (2)
 
+// NJ 32-column MFMA tiles per wave: a block covers BNW = 32 NJ kNW weight
+// columns (NJ = 2: 256, two blocks per CU; NJ = 1: 128, three blocks per CU).
+template <int NJ>
+struct Cols {
+    static constexpr int BNW = 32 * NJ * kNW;          // weight columns per block
+    static constexpr int B_I = 2 * BNW / 64 / kNW;     // weight DMA instructions per wave and group (NJ)
+    static constexpr int SB_I = 2 * BNW / (64 * kNW);  // scale/bias DMA instructions per wave and 8 groups (NJ)
+};
+
+template <int NJ>
 struct Stage {
     uint4 a[TBM * 8];                     // [row][chunk ^ ((row >> 1) & 7)], fp16 pairs
-    uint4 b[2 * BNW];                     // [32-column block][k-half][column]
+    uint4 b[2 * Cols<NJ>::BNW];           // [32-column block][k-half][column]
 };
 // Scales and biases of 8 groups: [scales | biases][weight column], 16 bytes
 // (groups 8 t .. 8 t + 7) each.
+template <int NJ>
 struct SbStage {
-    uint4 v[2][BNW];
+    uint4 v[2][Cols<NJ>::BNW];
 };
-static_assert(2 * sizeof(Stage) + 2 * sizeof(SbStage) <= 65536, "LDS DMA targets must lie in the first 64 KiB");
+static_assert(2 * sizeof(Stage<2>) + 2 * sizeof(SbStage<2>) <= 65536, "LDS DMA targets must lie in the first 64 KiB");
+static_assert(3 * (2 * sizeof(Stage<1>) + 2 * sizeof(SbStage<1>)) <= 160 * 1024, "three NJ = 1 blocks per CU");
 
 __device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
     __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
@@ -143,12 +151,16 @@ __device__ __forceinline__ void mfma_result_pad() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
+template <int EPI, int NJ>
+__global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Gemm16Args p) {
 #pragma clang fp contract(off)
     static_assert(EPI == GEMM_SWIGLU || EPI == GEMM_RESIDUAL, "the epilogues of mq4_mlp_residual");
+    static_assert(NJ == 2 || (NJ == 1 && EPI == GEMM_RESIDUAL), "SwiGLU: a gate and an up tile per wave");
     constexpr int NMAT = EPI == GEMM_SWIGLU ? 2 : 1;
+    constexpr int BNW = Cols<NJ>::BNW, B_I = Cols<NJ>::B_I, SB_I = Cols<NJ>::SB_I;
     constexpr int BN = BNW / NMAT;                       // output columns per block
+    using Stage = g16::Stage<NJ>;
+    using SbStage = g16::SbStage<NJ>;
     __shared__ Stage st0, st1;
     __shared__ SbStage sb0, sb1;
 
@@ -242,34 +254,34 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     const bool f16_out = EPI == GEMM_SWIGLU && p.yscale != 0.0f;
     const bool paired_out = EPI == GEMM_SWIGLU && !f16_out && p.ysum != nullptr;
     const int ccol = f16_out || paired_out ? ((col & ~7) | perm8(col & 7)) : col;
-    int wr[2];
+    int wr[NJ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wave * 32 + ccol : wave * 64 + j * 32 + ccol;
+    for (int j = 0; j < NJ; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wave * 32 + ccol : wave * (32 * NJ) + j * 32 + ccol;
 
     uint32_t nib_mask, nib_exp;               // the nibble-pair constants, set up once
     asm("s_mov_b32 %0, 0x000f000f" : "=s"(nib_mask));
     asm("v_mov_b32 %0, 0x64006400" : "=v"(nib_exp));
 
-    f32x16_t acc[4][2];
+    f32x16_t acc[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     // this group's packed words, scales and biases (read before the step's
     // DMA is issued, so no wait for it can come between)
     struct Wts {
-        uint4 bw[2];
-        h2_t s2[2], b2[2];
+        uint4 bw[NJ];
+        h2_t s2[NJ], b2[NJ];
     };
     auto load_wts = [&](int g, const Stage& st) -> Wts {
         Wts w;
         const SbStage& sbs = ((g >> 3) & 1) ? sb1 : sb0;
         const int sh16 = (g & 1) * 16, dw = (g >> 1) & 3;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             w.bw[j] = st.b[(wr[j] >> 5) * 64 + h * 32 + (wr[j] & 31)];
             const _Float16 s = bf16_to_h((reinterpret_cast<const uint32_t*>(&sbs.v[0][wr[j]])[dw] >> sh16) & 0xffffu);
             const _Float16 b = bf16_to_h((reinterpret_cast<const uint32_t*>(&sbs.v[1][wr[j]])[dw] >> sh16) & 0xffffu);
@@ -294,30 +306,30 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
                 a[i] = __builtin_bit_cast(h8_t, st.a[r * 8 + (ch ^ ((r >> 1) & 7))]);
             }
         };
-        auto dequant = [&](int ks, h8_t (&bo)[2]) {
+        auto dequant = [&](int ks, h8_t (&bo)[NJ]) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < NJ; ++j) {
                 const uint32_t w = ks == 0 ? bw[j].x : ks == 1 ? bw[j].y : ks == 2 ? bw[j].z : bw[j].w;
                 bo[j] = dequant_word(w, s2[j], b2[j], nib_mask, nib_exp);
             }
         };
-        auto mfmas = [&](const h8_t (&a)[4], const h8_t (&bo)[2]) {
+        auto mfmas = [&](const h8_t (&a)[4], const h8_t (&bo)[NJ]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < NJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bo[j], a[i], acc[i][j], 0, 0, 0);
         };
         auto interleave = [] {
 #pragma unroll
-            for (int m = 0; m < 8; ++m) {
+            for (int m = 0; m < 4 * NJ; ++m) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
                 if (m < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // LDS read
                 __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                 // VALU
             }
             __builtin_amdgcn_sched_barrier(0);
         };
-        h8_t a0[4], a1[4], w0[2], w1[2];
+        h8_t a0[4], a1[4], w0[NJ], w1[NJ];
         read_a(0, a0);
         dequant(0, w0);
         read_a(1, a1);
@@ -391,15 +403,15 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
     // lane, the read first.
     constexpr bool kResRuns = EPI == GEMM_RESIDUAL;
     const bool res_runs = kResRuns && S == 1;
-    uint2 resv[4][8];
+    uint2 resv[4][4 * NJ];
     const bool res_whole = vec && n0 + BN <= N;          // every run of the block: one 8-byte load
-    auto load_res = [&](int i, uint2 (&rv)[8]) {
+    auto load_res = [&](int i, uint2 (&rv)[4 * NJ]) {
         const int row = m0 + i * 32 + col;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int eg = 0; eg < 4; ++eg) {
-                const int cb = n0 + wave * 64 + j * 32 + eg * 8 + h * 4;
+                const int cb = n0 + wave * (32 * NJ) + j * 32 + eg * 8 + h * 4;
                 uint2 t = make_uint2(0u, 0u);
                 if (row < M && cb < N) {
                     const uint16_t* r = p.res + (int64_t)row * N + cb;
@@ -422,9 +434,9 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = m0 + i * 32 + col;
-                const uint16_t* r = p.res + (int64_t)(row < M ? row : M - 1) * N + n0 + wave * 64 + h * 4;
+                const uint16_t* r = p.res + (int64_t)(row < M ? row : M - 1) * N + n0 + wave * (32 * NJ) + h * 4;
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < NJ; ++j)
 #pragma unroll
                     for (int eg = 0; eg < 4; ++eg)
                         resv[i][j * 4 + eg] = *reinterpret_cast<const uint2*>(r + j * 32 + eg * 8);
@@ -455,10 +467,10 @@ __global__ __launch_bounds__(kThreads, 2) void q4_gemm16_kernel(Gemm16Args p) {
             swiglu_bf16_batch<16>(ga, ua, hv);
         }
 #pragma unroll
-        for (int j = 0; j < (NMAT == 2 ? 1 : 2); ++j) {
+        for (int j = 0; j < (NMAT == 2 ? 1 : NJ); ++j) {
 #pragma unroll
             for (int eg = 0; eg < 4; ++eg) {
-                const int cl = (NMAT == 2 ? wave * 32 : wave * 64 + j * 32) + eg * 8 + h * 4;
+                const int cl = (NMAT == 2 ? wave * 32 : wave * (32 * NJ) + j * 32) + eg * 8 + h * 4;
                 const int cb = n0 + cl;                             // first column (position) of the run
                 if (cb >= N) continue;
                 const bool whole = vec && cb + 3 < N;
@@ -718,11 +730,19 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
                   reinterpret_cast<uintptr_t>(a.part) % 16 != 0 || a.N % 4 != 0 || !aligned(a.res, 8) ||
                   !aligned(a.y, 8)))
         return -1;
-    const int BN = epi == GEMM_SWIGLU ? g16::BNW / 2 : g16::BNW;
+    // 128-column tiles (three blocks per CU) for the residual product when
+    // asked for, else 256
+    const bool narrow = epi == GEMM_RESIDUAL && a.narrow;
+    const int BN = epi == GEMM_SWIGLU ? g16::Cols<2>::BNW / 2 : narrow ? g16::Cols<1>::BNW : g16::Cols<2>::BNW;
     const unsigned blocks = (unsigned)(((a.N + BN - 1) / BN) * ((a.M + g16::TBM - 1) / g16::TBM) * S);
     switch (epi) {
         case GEMM_RESIDUAL: {
-            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_RESIDUAL>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
+            if (narrow)
+                hipLaunchKernelGGL((g16::q4_gemm16_kernel<GEMM_RESIDUAL, 1>), dim3(blocks), dim3(g16::kThreads), 0, st,
+                                   a);
+            else
+                hipLaunchKernelGGL((g16::q4_gemm16_kernel<GEMM_RESIDUAL, 2>), dim3(blocks), dim3(g16::kThreads), 0, st,
+                                   a);
             if (S > 1) {
                 const int64_t MN = (int64_t)a.M * a.N;
                 hipLaunchKernelGGL(g16::kpart_residual_kernel, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,
@@ -731,7 +751,7 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
             return 0;
         }
         case GEMM_SWIGLU:
-            hipLaunchKernelGGL(g16::q4_gemm16_kernel<GEMM_SWIGLU>, dim3(blocks), dim3(g16::kThreads), 0, st, a);
+            hipLaunchKernelGGL((g16::q4_gemm16_kernel<GEMM_SWIGLU, 2>), dim3(blocks), dim3(g16::kThreads), 0, st, a);
             return 0;
         default:
             return -1;

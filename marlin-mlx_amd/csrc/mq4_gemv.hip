@@ -767,17 +767,29 @@ struct MlpWs {
     size_t bytes = 0;
 };
 
-// K parts of the fp16-weight down product ([M, N] . [K, N]^T, N / 64 groups)
-// on the one-call path: the most of 1, 2 and 4 (whole 8-group scale slots
-// per part) whose 128 x 256 tiles times parts stay within one block per CU.
-// Measured on the 2048 x 6144 down product with its part combine: M = 1024,
-// 64 tiles: 90 / 54 / 45 us for 1 / 2 / 4 parts; M = 2048, 128 tiles: 93 /
-// 71 / 75 us; M = 4096, 256 tiles: 121 / 124 / 141 us.  0: N / 64 not a
-// multiple of 8 (no fp16 down product).
+// Tiles and K parts of the fp16-weight down product ([M, N] . [K, N]^T,
+// N / 64 groups) on the one-call path: 128 x 128 tiles (three blocks per CU)
+// while there are at most two of them per CU, else 128 x 256; and the most
+// of 1, 2 and 4 parts (whole 8-group scale slots per part) whose tiles times
+// parts stay within one block per CU.  Measured on the 2048 x 6144 down
+// product with its part combine, us for 1 / 2 / 4 parts, 128 x 256 tiles then
+// 128 x 128:
+//   M = 200:  84.4 / 48.6 / 31.0,    55.2 / 33.2 / 22.5
+//   M = 1024: 91.7 / 54.8 / 45.6,    61.0 / 42.7 / 45.0
+//   M = 2048: 99.1 / 71.2 / 79.1,    69.8 / 71.2 / 80.4
+//   M = 3072: 108.0 / 105.0 / 113.4, 101.4 / 101.6 / 114.8
+//   M = 4096: 119.5 / 126.2 / 146.4, 118.0 / 133.3 / 150.9
+//   M = 8192: 212.5 / 250.5 / 315.0, 230.4 / 268.6 / 332.4
+// Either tile width gives the same bits.  0 parts: N / 64 not a multiple of
+// 8 (no fp16 down product).
+static bool mlp_down_narrow(int64_t M, int64_t K) {
+    return ((M + 127) / 128) * ((K + 127) / 128) <= 2 * (int64_t)num_cus();
+}
 static int mlp_down_parts(int64_t M, int64_t K, int64_t N) {
     const int64_t G = N / 64;
     if (N % 64 != 0 || G % 8 != 0) return 0;
-    const int64_t tiles = ((M + 127) / 128) * ((K + 255) / 256);
+    const int64_t BN = mlp_down_narrow(M, K) ? 128 : 256;
+    const int64_t tiles = ((M + 127) / 128) * ((K + BN - 1) / BN);
     int S = 1;
     for (int s : {2, 4})
         if ((G / 8) % s == 0 && tiles * s <= (int64_t)num_cus()) S = s;
@@ -865,9 +877,9 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
         // SwiGLU on an fp16 copy of the normalized x (its per-row
         // power-of-two scales in the xs area), and the down product on h
         // written as fp16 / 256 in the operand order (exact for |h| in
-        // [2^-6, 1.6e7]), in mlp_down_parts K parts (2048 x 6144 down at M =
-        // 2048: 71 us in two parts, against 102 us on the exact-operand GEMM
-        // with paired bf16 h).  With the down product's scale or bias rows
+        // [2^-6, 1.6e7]), with the tiles and K parts of mlp_down_parts (2048
+        // x 6144 down at M = 2048: 70 us, against 102 us on the
+        // exact-operand GEMM with paired bf16 h).  With the down product's scale or bias rows
         // not 16-byte aligned, gate/up writes h paired in bf16 with its group
         // sums for the exact-operand GEMM's down product.
         auto a16 = [](const QMat& q) { return aligned(q.s, 16) && aligned(q.b, 16); };
@@ -885,7 +897,7 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
             if (down16) {
                 Gemm16Args dn{w.hp, nullptr, (int)M, (int)K, (int)N, D, QMat{nullptr, nullptr, nullptr}, y, x,
-                              nullptr, 256.0f, 0.0f, parts, w.kpart};
+                              nullptr, 256.0f, 0.0f, parts, w.kpart, mlp_down_narrow(M, K) ? 1 : 0};
                 if (launch_q4_gemm16(dn, GEMM_RESIDUAL, st))
                     return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
                 return launch_status(what);

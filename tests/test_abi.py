@@ -224,8 +224,9 @@ def test_mlp_residual_workspace_and_validation(mq4):
     """mq4_mlp_workspace_size: h [M, N] bf16, plus for 5-32 rows the two fp32
     K parts of the down product [2, M, K], and from 33 rows on the paired x
     [M, K], the group sums of x and h and the fp16-weight down product's
-    fp32 K parts [S, M, K] (S of 1, 2, 4 with ceil(M / 128) ceil(K / 256) S
-    <= 256 CUs; no section for S = 1), each section 256-byte aligned; the
+    fp32 K parts [S, M, K] (S of 1, 2, 4 with tiles x S <= 256 CUs, the
+    tiles 128 x 128 while ceil(M / 128) ceil(K / 128) <= 512, else 128 x
+    256; no section for S = 1), each section 256-byte aligned; the
     entry rejects a missing, small or misaligned workspace (and bad shapes)
     before enqueueing anything."""
     L = mq4.lib()
@@ -236,18 +237,23 @@ def test_mlp_residual_workspace_and_validation(mq4):
     assert L.mq4_mlp_workspace_size(32, 2048, 6144) == up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
     M, K, N = 2048, 2048, 6144
     # from 33 rows: h, the paired (or fp16) operand, its group sums (or row
-    # scales), h's group sums and (M = 2048: 16 x 8 tiles) two K parts
+    # scales), h's group sums and the K parts (M = 2048: 16 x 16 tiles of
+    # 128 x 128, one part, no section)
     assert L.mq4_mlp_workspace_size(M, K, N) == (up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) +
-                                                 up(M * N // 64 * 4) + up(2 * M * K * 4))
-    # 8192 rows (512 tiles): one part, no section
+                                                 up(M * N // 64 * 4))
+    # 1000 rows: 8 x 16 tiles, two parts
+    M1 = 1000
+    assert L.mq4_mlp_workspace_size(M1, K, N) >= (up(M1 * N * 2) + up(M1 * K * 2) + up(M1 * K // 64 * 4) +
+                                                  up(M1 * N // 64 * 4) + up(2 * M1 * K * 4))
+    # 8192 rows (64 x 8 tiles of 128 x 256): one part, no section
     M8 = 8192
     assert L.mq4_mlp_workspace_size(M8, K, N) == (up(M8 * N * 2) + up(M8 * K * 2) + up(M8 * K // 64 * 4) +
                                                   up(M8 * N // 64 * 4))
     # the size for M rows covers every smaller row count, also where the
-    # K-part count drops (1024 rows: four parts)
+    # K-part count drops (512 rows: four parts, 513: two)
     big = L.mq4_mlp_workspace_size(3000, K, N)
-    assert all(L.mq4_mlp_workspace_size(m, K, N) <= big for m in (33, 1024, 1025, 2048, 2049, 3000))
-    assert L.mq4_mlp_workspace_size(1024, K, N) >= up(4 * 1024 * K * 4)
+    assert all(L.mq4_mlp_workspace_size(m, K, N) <= big for m in (33, 512, 513, 1024, 1025, 2048, 2049, 3000))
+    assert L.mq4_mlp_workspace_size(600, K, N) >= up(4 * 512 * K * 4)
     # the size for M rows covers every call of at most M rows (the paired
     # GEMM regime from 33 rows needs less per row than the two fp32 K parts of
     # 5-32 rows, so the size is the largest over the regimes up to M)
