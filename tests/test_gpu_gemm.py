@@ -200,13 +200,13 @@ def test_gemm_epilogues_at_prefill_m(mq4, O, dev):
 def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
     """mq4_mlp_residual: x + mlp_forward(rms_norm(x)) in one call
     (src/model/marlin.cpp:141-142).  From 33 rows on with K, N multiples of 512
-    it runs the GEMM on operands stored in the matrix cores' order with their
-    group sums ((1960, 2048, 6144), (200, ...), (40, 512, 1024)); the down +
-    residual product of that path takes 64 x 32 wave tiles while 64 x 64 tiles
-    would leave at most one block per CU (M <= 2048 at N = 2048) and 64 x 64
-    tiles above that: (4096, ...) and (8192, ...) (512 and 1024 blocks of
-    128 x 128 on 256 CUs), the prefill bench's M = 8192 figure, run the 64 x 64
-    instance, checked on sampled rows that include three of the last 128-row
+    and 16-byte aligned scales and biases both products run on the
+    fp16-weight GEMM on operands stored in the matrix cores' order; the down
+    + residual product on 128 x 128 tiles while they number at most two per
+    CU, in the most K parts that keep one block per CU ((1960, 2048, 6144) and
+    (4096, ...): one part; (200, ...): four; (40, 512, 1024): two), and on
+    128 x 256 tiles beyond ((8192, ...), the prefill bench's M = 8192
+    figure), checked on sampled rows that include three of the last 128-row
     tile (M - 1, M - 2, M - 40); (200, 2048, 1536): 12 gate/up column blocks
     (not a multiple of 8, the plain block order) and a 24-group down product
     in one part; (130, 1024, 2048): four down parts of one 8-group scale slot
@@ -263,14 +263,15 @@ def test_mlp_residual_one_call(mq4, O, dev, M, K, N):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,shift", [(200, "down"), (1960, "down"), (200, "gate")])
+@pytest.mark.parametrize("M,shift", [(200, "down"), (1960, "down"), (4096, "down"), (200, "gate")])
 def test_mlp_residual_paired_down(mq4, O, dev, M, shift):
     """The one-call MLP with one matrix's scales and biases 4-byte but not
     16-byte aligned.  down: gate/up on the fp16-weight GEMM writes h paired
     in bf16 (pair order through the per-chunk column permutation) with its
     group sums from the LDS tile, and the down product runs on the
-    exact-operand GEMM.  gate: both products on the exact-operand GEMM with
-    paired operands.  Against the separate entries: >= 95% of the bits
+    exact-operand GEMM (M = 4096: its 64 x 64 wave tiles, 512 blocks of
+    128 x 128; below: 64 x 32).  gate: both products on the exact-operand
+    GEMM with paired operands.  Against the separate entries: >= 95% of the bits
     identical, rms of the difference <= 1e-2 of the MLP output's rms; against
     the oracle chain on sampled rows: rms(err) <= 1e-2 of that rms."""
     import torch
@@ -319,6 +320,31 @@ def test_mlp_residual_paired_down(mq4, O, dev, M, shift):
     rel_o = float(np.sqrt(np.mean(err * err) / np.mean(mo * mo)))
     print(f"vs oracle chain: rms(err)/rms(mlp) {rel_o:.2e}")
     assert rel_o <= TOL
+
+
+@pytest.mark.gpu
+def test_mlp_residual_down_tile_widths_agree(mq4, O, dev):
+    """The one-call MLP's down product (2048 x 6144) runs on 128 x 128 tiles
+    while they number at most two per CU (2048 and 3000 rows: 256 and 384
+    tiles on 256 CUs) and on 128 x 256 tiles beyond (8192 rows), in one K
+    part each.  Every row's result depends only on that row (its norm, its
+    fp16 copy, its products in the same K order), so the 2048- and 3000-row
+    calls equal the first rows of the 8192-row call bit for bit (3000: a
+    ragged last tile of 56 rows)."""
+    import torch
+    K, N = 2048, 6144
+    print("mlp_residual tile widths M=8192 / 3000 / 2048", flush=True)
+    ws = [make(mq4, O, *((N, K) if p < 2 else (K, N)), 1500 + p, dev) for p in range(3)]
+    w = mq4.MLPWeights(*[mq4.QuantizedTensor(*d) for d, _ in ws])
+    x = mq4.fill_normal_bf16((8192, K), mq4.STREAM_PREFILL + 4, 0.0, 1.0, device=dev)
+    nw = mq4.fill_normal_bf16((K,), mq4.stream_id_layer_norm(4), 0.1, 0.02, device=dev)
+    full = mq4.mlp_residual(x, w, nw, 1e-6).view(torch.int16)
+    for M in (3000, 2048):
+        part = mq4.mlp_residual(x[:M], w, nw, 1e-6).view(torch.int16)
+        torch.cuda.synchronize()
+        same = float((part == full[:M]).float().mean())
+        print(f"M={M}: identical to the 8192-row call {same:.6f}")
+        assert torch.equal(part, full[:M])
 
 
 @pytest.mark.gpu
