@@ -401,8 +401,7 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
     // are loaded before the first is written (one wait, not one per run).
     // In place (res == y) every element is read and written by the same
     // lane, the read first.
-    constexpr bool kResRuns = EPI == GEMM_RESIDUAL;
-    const bool res_runs = kResRuns && S == 1;
+    const bool res_runs = EPI == GEMM_RESIDUAL && S == 1;
     uint2 resv[4][4 * NJ];
     const bool res_whole = vec && n0 + BN <= N;          // every run of the block: one 8-byte load
     auto load_res = [&](int i, uint2 (&rv)[4 * NJ]) {
@@ -427,7 +426,7 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
                 rv[j * 4 + eg] = t;
             }
     };
-    if (kResRuns && res_runs) {
+    if (res_runs) {
         if (res_whole) {
             // rows past M read row M - 1 (never stored): no branch between
             // the loads
