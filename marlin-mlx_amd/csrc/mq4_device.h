@@ -143,28 +143,25 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float g_acc, float u_acc) {
 }
 
 // round_bf16(1 / (1 + expf(-g))) for a bf16 value g, bit for bit, mostly
-// without expf and the IEEE division.  exp(-g) = 2^(xh + xl) with the
-// Cody-Waite split xh = -g L_HI (exact: 8 x 15 significant bits), xl = -g
-// L_LO; 2^xh on v_exp_f32, 2^xl = 1 + t + t^2 / 2 (t = xl ln 2, |t| < 2^-10
-// for |g| < 64); the reciprocal of 1 + e on v_rcp_f32 plus one Newton step.
-// That value r is within a few fp32 ulps of the exact formula's, so both
-// round to the same bf16 unless r's low 16 bits lie within SIG_MARGIN of
-// the rounding midpoint 0x8000; then, and for |g| >= 64 or non-finite g,
-// the exact formula is evaluated.  Checked against it for all 65536 bf16
-// values of g (tests/hip/mq4_device_check.hip).
-constexpr uint32_t SIG_MARGIN = 16;
+// without expf and the IEEE division: r = v_rcp_f32(1 + v_exp_f32(-g
+// log2(e))).  For |g| < 64 the rounded exponent -g log2(e) (|.| < 92.4, half
+// an ulp 2^-18) puts e within about 23 fp32 ulps of exp(-g) (relative
+// 2^-18 ln 2 plus v_exp_f32's own error), 1 + e keeps that relative bound,
+// and the reciprocal adds about one ulp: r lies within about 24 ulps of the
+// exact formula's value, so both round to the same bf16 unless r's low 16
+// bits lie within SIG_MARGIN = 32 of the rounding midpoint 0x8000; then, and
+// for |g| >= 64 or non-finite g, the exact formula is evaluated.  Checked
+// against it for all 65536 bf16 values of g (tests/hip/mq4_device_check.hip):
+// no mismatch, the fast value used for 34,038 of the 34,048 finite |g| < 64.
+// (A Cody-Waite split of the exponent with a second-order correction and a
+// Newton step on the reciprocal, within a few ulps, decided 34,041 with
+// SIG_MARGIN = 16 for four more instructions per value.)
+constexpr uint32_t SIG_MARGIN = 32;
 __device__ __forceinline__ bool sigmoid_bf16_fast(float g, float& s) {
 #pragma clang fp contract(off)
-    constexpr float L_HI = 0x1.7154p+0f;               // log2(e) to 15 significant bits
-    constexpr float L_LO = 0x1.d94ae0p-18f;            // log2(e) - L_HI
-    constexpr float LN2 = 0x1.62e430p-1f;
-    const float xh = -g * L_HI;
-    const float t = (-g * L_LO) * LN2;
-    float e = __builtin_amdgcn_exp2f(xh);
-    e = __builtin_fmaf(e, t + 0.5f * t * t, e);
+    const float e = __builtin_amdgcn_exp2f(g * -0x1.715476p+0f);   // -g log2(e), rounded
     const float d = 1.0f + e;
-    float r = __builtin_amdgcn_rcpf(d);
-    r = __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
+    const float r = __builtin_amdgcn_rcpf(d);
     // low 16 bits outside [0x8000 - SIG_MARGIN, 0x8000 + SIG_MARGIN]: one
     // unsigned compare of the wrapped offset
     const uint32_t lo = __builtin_bit_cast(uint32_t, r) & 0xffffu;
