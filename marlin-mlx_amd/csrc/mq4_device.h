@@ -142,71 +142,50 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float g_acc, float u_acc) {
     return f32_to_bf16(t * u);
 }
 
-// round_bf16(1 / (1 + expf(-g))) for a bf16 value g, bit for bit, mostly
-// without expf and the IEEE division: r = v_rcp_f32(1 + v_exp_f32(-g
-// log2(e))).  For |g| < 64 the rounded exponent -g log2(e) (|.| < 92.4, half
-// an ulp 2^-18) puts e within about 23 fp32 ulps of exp(-g) (relative
-// 2^-18 ln 2 plus v_exp_f32's own error), 1 + e keeps that relative bound,
-// and the reciprocal adds about one ulp: r lies within about 24 ulps of the
-// exact formula's value, so both round to the same bf16 unless r's low 16
-// bits lie within SIG_MARGIN = 32 of the rounding midpoint 0x8000; then, and
-// for |g| >= 64 or non-finite g, the exact formula is evaluated.  Checked
-// against it for all 65536 bf16 values of g (tests/hip/mq4_device_check.hip):
-// no mismatch, the fast value used for 34,038 of the 34,048 finite |g| < 64.
-// (A Cody-Waite split of the exponent with a second-order correction and a
-// Newton step on the reciprocal, within a few ulps, decided 34,041 with
-// SIG_MARGIN = 16 for four more instructions per value.)
-constexpr uint32_t SIG_MARGIN = 32;
-__device__ __forceinline__ bool sigmoid_bf16_fast(float g, float& s) {
+// swiglu_bf16 of N (gate, up) pairs through a table of the rounded SiLU
+// t(g) = round_bf16(round_bf16(1 / (1 + expf(-g))) * g), the same bits.  The
+// table holds t for the bf16 g with 2^-9 <= |g| < 128 (exponent fields
+// 118-133; entry (sign << 11) | (exponent - 118) << 7 | mantissa, 4096 x 2
+// bytes, silu_lut_entry).  Below 2^-9 the rounded sigmoid is 0.5 exactly, so
+// t = g / 2: the exponent field less one for exponent fields 2-117, and
+// +-0 for +-0.  The rest (|g| >= 128, inf, NaN, and |g| < 2^-125 where g / 2
+// is subnormal) take the exact formula, in one branch for the batch.
+constexpr int SILU_LUT_N = 4096;
+constexpr uint32_t SILU_LUT_LO = 118u << 7;          // |g| bits of 2^-9
+__device__ __forceinline__ uint32_t silu_lut_entry(uint32_t i) {
 #pragma clang fp contract(off)
-    const float e = __builtin_amdgcn_exp2f(g * -0x1.715476p+0f);   // -g log2(e), rounded
-    const float d = 1.0f + e;
-    const float r = __builtin_amdgcn_rcpf(d);
-    // low 16 bits outside [0x8000 - SIG_MARGIN, 0x8000 + SIG_MARGIN]: one
-    // unsigned compare of the wrapped offset
-    const uint32_t lo = __builtin_bit_cast(uint32_t, r) & 0xffffu;
-    s = round_bf16(r);
-    return __builtin_fabsf(g) < 64.0f && lo - (0x8000u - SIG_MARGIN) > 2u * SIG_MARGIN;
+    const uint32_t bits = ((i >> 11) << 15) | (SILU_LUT_LO + (i & 2047u));
+    const float g = bf16_to_f32(bits);
+    return f32_to_bf16(round_bf16(1.0f / (1.0f + expf(-g))) * g);
 }
-__device__ __forceinline__ float sigmoid_bf16(float g) {
-#pragma clang fp contract(off)
-    float s;
-    if (!sigmoid_bf16_fast(g, s)) s = round_bf16(1.0f / (1.0f + expf(-g)));
-    return s;
-}
-
-// swiglu_bf16 of N (gate, up) pairs, the same bits: the fast sigmoid of all
-// of them first, then the exact formula for those it did not decide, in one
-// branch for the batch (a branch per value splits the batch's exp and rcp
-// chains into regions the compiler cannot interleave).
 template <int N>
-__device__ __forceinline__ void swiglu_bf16_batch(const float (&g_acc)[N], const float (&u_acc)[N],
-                                                  uint32_t (&out)[N]) {
+__device__ __forceinline__ void swiglu_bf16_lut_batch(const float (&g_acc)[N], const float (&u_acc)[N],
+                                                      uint32_t (&out)[N], const uint16_t* lut) {
 #pragma clang fp contract(off)
     static_assert(N <= 32, "one mask word");
-    float g[N], s[N];
+    uint32_t gb[N], tb[N];
     uint32_t need = 0;
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-        g[e] = round_bf16(g_acc[e]);
-        if (!sigmoid_bf16_fast(g[e], s[e])) need |= 1u << e;
+        gb[e] = f32_to_bf16(g_acc[e]);
+        const uint32_t mag = gb[e] & 0x7fffu;
+        const uint32_t k = mag - SILU_LUT_LO;                            // unsigned
+        const uint32_t idx = (k < 2048u ? k : 0u) | ((gb[e] >> 4) & 0x800u);
+        const uint32_t lt = lut[idx];
+        const bool half = mag - 0x100u < SILU_LUT_LO - 0x100u;           // exponent fields 2-117
+        tb[e] = k < 2048u ? lt : half ? gb[e] - 0x80u : gb[e];           // +-0 keeps its bits
+        if (k >= 2048u && !half && mag != 0u) need |= 1u << e;
     }
     if (need) {
 #pragma unroll
         for (int e = 0; e < N; ++e)
-            if (need & (1u << e)) s[e] = round_bf16(1.0f / (1.0f + expf(-g[e])));
+            if (need & (1u << e)) {
+                const float g = bf16_to_f32(gb[e]);
+                tb[e] = f32_to_bf16(round_bf16(1.0f / (1.0f + expf(-g))) * g);
+            }
     }
 #pragma unroll
-    for (int e = 0; e < N; ++e) out[e] = f32_to_bf16(round_bf16(s[e] * g[e]) * round_bf16(u_acc[e]));
-}
-
-// swiglu_bf16 with sigmoid_bf16: the same bits.
-__device__ __forceinline__ uint32_t swiglu_bf16_fast(float g_acc, float u_acc) {
-#pragma clang fp contract(off)
-    const float g = round_bf16(g_acc);
-    const float u = round_bf16(u_acc);
-    const float t = round_bf16(sigmoid_bf16(g) * g);
-    return f32_to_bf16(t * u);
+    for (int e = 0; e < N; ++e) out[e] = f32_to_bf16(bf16_to_f32(tb[e]) * round_bf16(u_acc[e]));
 }
 
 // Monotone 16-bit key of a bf16 value for max-selection: larger value ->

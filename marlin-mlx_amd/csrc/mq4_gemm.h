@@ -65,6 +65,9 @@ struct Gemm16Args {
     // GEMM_RESIDUAL: nonzero for blocks of 128 weight columns (one 32-column
     // MFMA tile per wave, three blocks per CU) instead of 256; the same bits
     int narrow;
+    // GEMM_SWIGLU: the 4096-entry SiLU table of silu_lut_entry (16-byte
+    // aligned; launch_pair_rows16 writes it)
+    const uint16_t* silu_lut;
 };
 
 // Enqueue the fp16-weight GEMM (GEMM_SWIGLU or GEMM_RESIDUAL, the products of
@@ -77,9 +80,10 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st);
 // eps) * (1 + norm_w)) / xscale[m]) in the operand order (the bits of
 // mq4_rms_norm before the conversion), with xscale[m] = 2^e, e >= 0 the
 // smallest that keeps the row below 2^15.  K % 512 == 0; x, xp, norm_w
-// 16-byte aligned.
+// 16-byte aligned.  silu_lut non-null: the same launch also writes the
+// SiLU table of GEMM_SWIGLU (SILU_LUT_N entries).
 int launch_pair_rows16(const uint16_t* x, int M, int K, const uint16_t* norm_w, float eps, uint16_t* xp,
-                       float* xscale, hipStream_t st);
+                       float* xscale, uint16_t* silu_lut, hipStream_t st);
 
 // xp = x (norm_w null) or bf16(x * rsqrt(mean(x^2) + eps) * (1 + norm_w)),
 // the bits of mq4_rms_norm, with every 8-element chunk of a row in the

@@ -161,8 +161,17 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
     constexpr int BN = BNW / NMAT;                       // output columns per block
     using Stage = g16::Stage<NJ>;
     using SbStage = g16::SbStage<NJ>;
-    __shared__ Stage st0, st1;
-    __shared__ SbStage sb0, sb1;
+    // one LDS object, stages first: the DMA targets stay in the first 64 KiB
+    // (SwiGLU: the 8 KB SiLU table after them, read only by the epilogue)
+    struct Smem {
+        Stage st[2];
+        SbStage sb[2];
+        uint16_t lut[EPI == GEMM_SWIGLU ? SILU_LUT_N : 2];
+    };
+    __shared__ Smem smem;
+    Stage &st0 = smem.st[0], &st1 = smem.st[1];
+    SbStage &sb0 = smem.sb[0], &sb1 = smem.sb[1];
+    static_assert(2 * sizeof(Stage) + 2 * sizeof(SbStage) <= 65536, "LDS DMA targets in the first 64 KiB");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -360,8 +369,23 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
         if ((g & 7) == 0 && g + 8 < GL) issue_sb((g >> 3) + 1, ((g >> 3) & 1) ? sb0 : sb1);
         compute(wt, cur);
     };
+    // the SiLU table (SwiGLU) is loaded with group 0 and stored to LDS after
+    // its wait; the first step's barrier publishes it
+    uint4 lut0 = make_uint4(0, 0, 0, 0), lut1 = lut0;
+    if (EPI == GEMM_SWIGLU) {
+        static_assert(SILU_LUT_N * 2 == 2 * 16 * kThreads, "two 16-byte pieces of the table per thread");
+        const uint4* src = reinterpret_cast<const uint4*>(p.silu_lut);
+        lut0 = src[tid];
+        lut1 = src[tid + kThreads];
+    }
     issue(0, st0);
     issue_sb(0, sb0);
+    if (EPI == GEMM_SWIGLU) {
+        wait_vmcnt<0>();
+        uint4* dst = reinterpret_cast<uint4*>(smem.lut);
+        dst[tid] = lut0;
+        dst[tid + kThreads] = lut1;
+    }
     int g0 = 0;
     for (; g0 + 2 <= GL; g0 += 2) {
         step(g0, st0, st1);
@@ -463,7 +487,7 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
                 ga[e] = acc[i][0][e] * sc;
                 ua[e] = acc[i][1][e] * sc;
             }
-            swiglu_bf16_batch<16>(ga, ua, hv);
+            swiglu_bf16_lut_batch<16>(ga, ua, hv, smem.lut);
         }
 #pragma unroll
         for (int j = 0; j < (NMAT == 2 ? 1 : NJ); ++j) {
@@ -576,12 +600,21 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
 // 2^15 (0 for every normalized row whose values stay below 2^15).  With CAP >
 // 0 (K <= 512 CAP) a lane keeps its chunks of x and of the norm weight in
 // registers between the passes (all loads issued first), so the row is read
-// once; the sums keep the chunk order of the reloading form (CAP = 0).
+// once; the sums keep the chunk order of the reloading form (CAP = 0).  With
+// lut, the blocks past the rows' write the SiLU table (silu_lut_entry), one
+// entry per thread.
 template <bool NORM, int CAP>
 __global__ __launch_bounds__(256) void pair_rows16_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                           const uint16_t* __restrict__ nw, float eps,
-                                                          uint16_t* __restrict__ xp, float* __restrict__ xscale) {
+                                                          uint16_t* __restrict__ xp, float* __restrict__ xscale,
+                                                          uint16_t* __restrict__ lut) {
 #pragma clang fp contract(off)
+    const int row_blocks = (M + 3) / 4;
+    if ((int)blockIdx.x >= row_blocks) {
+        const uint32_t i = (blockIdx.x - (uint32_t)row_blocks) * 256u + threadIdx.x;
+        if (i < (uint32_t)SILU_LUT_N) lut[i] = (uint16_t)silu_lut_entry(i);
+        return;
+    }
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= M) return;                                  // whole waves
@@ -693,23 +726,23 @@ __global__ __launch_bounds__(256) void kpart_residual_kernel(const float* __rest
 }  // namespace g16
 
 int launch_pair_rows16(const uint16_t* x, int M, int K, const uint16_t* norm_w, float eps, uint16_t* xp,
-                       float* xscale, hipStream_t st) {
+                       float* xscale, uint16_t* silu_lut, hipStream_t st) {
     if (M < 1 || K % 512 != 0) return -1;
-    const unsigned blocks = (unsigned)((M + 3) / 4);
+    const unsigned blocks = (unsigned)((M + 3) / 4) + (silu_lut ? (unsigned)(SILU_LUT_N / 256) : 0u);
     // rows of at most 4 chunks per lane (K <= 2048) read once
     const bool cached = K / 512 <= 4;
     if (norm_w && cached)
         hipLaunchKernelGGL((g16::pair_rows16_kernel<true, 4>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
-                           xp, xscale);
+                           xp, xscale, silu_lut);
     else if (norm_w)
         hipLaunchKernelGGL((g16::pair_rows16_kernel<true, 0>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
-                           xp, xscale);
+                           xp, xscale, silu_lut);
     else if (cached)
         hipLaunchKernelGGL((g16::pair_rows16_kernel<false, 4>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
-                           xp, xscale);
+                           xp, xscale, silu_lut);
     else
         hipLaunchKernelGGL((g16::pair_rows16_kernel<false, 0>), dim3(blocks), dim3(256), 0, st, x, M, K, norm_w, eps,
-                           xp, xscale);
+                           xp, xscale, silu_lut);
     return 0;
 }
 
@@ -721,6 +754,7 @@ int launch_q4_gemm16(const Gemm16Args& a, int epi, hipStream_t st) {
     if (!fits32 || a.K % 512 != 0 || a.M < 1 || a.N < 1 || !a16(a.A) || (epi == GEMM_SWIGLU && !a16(a.B))) return -1;
     if (a.ysum && (epi != GEMM_SWIGLU || a.yscale != 0.0f || a.N % 128 != 0)) return -1;
     if (a.yscale != 0.0f && (epi != GEMM_SWIGLU || a.N % 8 != 0)) return -1;
+    if (epi == GEMM_SWIGLU && (!a.silu_lut || !aligned(a.silu_lut, 16))) return -1;
     // K parts: GEMM_RESIDUAL only, at most 4, whole 8-group scale slots per
     // part, fp32 parts [ksplit][M][N] (16-byte aligned, N % 4 == 0) combined
     // by a second kernel

@@ -755,7 +755,9 @@ namespace mq4 {
 // forms them per wave.  On the MFMA GEMV path (kMfmaMinM <= M < kGemmMinM)
 // part [2, M, K] fp32 holds the two K parts of the split down product.  On
 // the fp16-weight path the down product in S > 1 K parts puts them in
-// kpart [S, M, K] fp32.  Sections 256-byte aligned.
+// kpart [S, M, K] fp32, and silu holds the SwiGLU epilogue's table of the
+// rounded SiLU (SILU_LUT_N bf16, written by the pre-pass).  Sections 256-byte
+// aligned.
 struct MlpWs {
     uint16_t* h = nullptr;
     uint16_t* xp = nullptr;
@@ -764,6 +766,7 @@ struct MlpWs {
     float* hs = nullptr;
     float* part = nullptr;
     float* kpart = nullptr;
+    uint16_t* silu = nullptr;
     size_t bytes = 0;
 };
 
@@ -813,6 +816,7 @@ static MlpWs mlp_ws_layout(void* base, int64_t M, int64_t K, int64_t N) {
         w.hs = reinterpret_cast<float*>(take((size_t)M * (N / 64) * 4));
         const int S = mlp_down_parts(M, K, N);
         if (S > 1) w.kpart = reinterpret_cast<float*>(take((size_t)S * M * K * 4));
+        w.silu = reinterpret_cast<uint16_t*>(take((size_t)SILU_LUT_N * 2));
     } else if (M >= kMfmaMinM) {
         w.part = reinterpret_cast<float*>(take((size_t)2 * M * K * 4));
     }
@@ -889,10 +893,10 @@ extern "C" int mq4_mlp_residual(const uint16_t* x, int64_t M, int64_t K, const u
             int parts = a16(D) ? mlp_down_parts(M, K, N) : 0;
             if (parts > 1 && !aligned(y, 8)) parts = 1;
             const bool down16 = parts > 0;
-            if (launch_pair_rows16(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, st))
+            if (launch_pair_rows16(x, (int)M, (int)K, norm_weight, eps, w.xp, w.xs, w.silu, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
             Gemm16Args gu{w.xp, w.xs, (int)M, (int)N, (int)K, G, U, w.hp, nullptr, down16 ? nullptr : w.hs, 0.0f,
-                          down16 ? 1.0f / 256.0f : 0.0f};
+                          down16 ? 1.0f / 256.0f : 0.0f, 0, nullptr, 0, w.silu};
             if (launch_q4_gemm16(gu, GEMM_SWIGLU, st))
                 return fail(MQ4_ERR_UNSUPPORTED, "%s: unsupported shape", what);
             if (down16) {

@@ -226,7 +226,8 @@ def test_mlp_residual_workspace_and_validation(mq4):
     [M, K], the group sums of x and h and the fp16-weight down product's
     fp32 K parts [S, M, K] (S of 1, 2, 4 with tiles x S <= 256 CUs, the
     tiles 128 x 128 while ceil(M / 128) ceil(K / 128) <= 512, else 128 x
-    256; no section for S = 1), each section 256-byte aligned; the
+    256; no section for S = 1) and the SwiGLU epilogue's SiLU table (4096
+    bf16), each section 256-byte aligned; the
     entry rejects a missing, small or misaligned workspace (and bad shapes)
     before enqueueing anything."""
     L = mq4.lib()
@@ -237,18 +238,19 @@ def test_mlp_residual_workspace_and_validation(mq4):
     assert L.mq4_mlp_workspace_size(32, 2048, 6144) == up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
     M, K, N = 2048, 2048, 6144
     # from 33 rows: h, the paired (or fp16) operand, its group sums (or row
-    # scales), h's group sums and the K parts (M = 2048: 16 x 16 tiles of
-    # 128 x 128, one part, no section)
+    # scales), h's group sums, the K parts (M = 2048: 16 x 16 tiles of
+    # 128 x 128, one part, no section) and the SiLU table
+    lut = 4096 * 2
     assert L.mq4_mlp_workspace_size(M, K, N) == (up(M * N * 2) + up(M * K * 2) + up(M * K // 64 * 4) +
-                                                 up(M * N // 64 * 4))
+                                                 up(M * N // 64 * 4) + lut)
     # 1000 rows: 8 x 16 tiles, two parts
     M1 = 1000
     assert L.mq4_mlp_workspace_size(M1, K, N) >= (up(M1 * N * 2) + up(M1 * K * 2) + up(M1 * K // 64 * 4) +
-                                                  up(M1 * N // 64 * 4) + up(2 * M1 * K * 4))
+                                                  up(M1 * N // 64 * 4) + up(2 * M1 * K * 4) + lut)
     # 8192 rows (64 x 8 tiles of 128 x 256): one part, no section
     M8 = 8192
     assert L.mq4_mlp_workspace_size(M8, K, N) == (up(M8 * N * 2) + up(M8 * K * 2) + up(M8 * K // 64 * 4) +
-                                                  up(M8 * N // 64 * 4))
+                                                  up(M8 * N // 64 * 4) + lut)
     # the size for M rows covers every smaller row count, also where the
     # K-part count drops (512 rows: four parts, 513: two)
     big = L.mq4_mlp_workspace_size(3000, K, N)
@@ -263,7 +265,7 @@ def test_mlp_residual_workspace_and_validation(mq4):
     assert L.mq4_mlp_workspace_size(40, 2048, 6144) >= up(32 * 6144 * 2) + up(2 * 32 * 2048 * 4)
     # the call itself needs only its own row count's layout (40 rows: the
     # paired GEMM operands), less than the size that covers every M <= 40
-    need = up(40 * 6144 * 2) + up(40 * 2048 * 2) + up(40 * 2048 // 64 * 4) + up(40 * 6144 // 64 * 4)
+    need = up(40 * 6144 * 2) + up(40 * 2048 * 2) + up(40 * 2048 // 64 * 4) + up(40 * 6144 // 64 * 4) + lut
     assert need < L.mq4_mlp_workspace_size(40, 2048, 6144)
     w = [fake(A16)] * 9
     call = lambda ws, nb, **kw: L.mq4_mlp_residual(kw.get("x", fake(A16)), kw.get("M", 40), kw.get("K", 2048),
