@@ -117,9 +117,9 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
 // normal range)
 __device__ __forceinline__ _Float16 bf16_to_h(uint32_t bits) { return (_Float16)bf16_to_f32(bits); }
 
-// fp16 (1024 + q_p, 1024 + q_{p+4}) of nibbles p, p + 4 of s: one
-// v_and_or_b32 with the mask in an SGPR and the exponent bits in a VGPR,
-// both set up once by the caller.
+// (s & m) | c in one v_and_or_b32, the mask in an SGPR and the exponent
+// bits in a VGPR, both set up once by the caller: the nibbles m selects in
+// each 16-bit half as fp16 mantissa bits under c's exponents.
 __device__ __forceinline__ uint32_t nib_pair_h(uint32_t s, uint32_t m, uint32_t c) {
     uint32_t r;
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(s), "s"(m), "v"(c));
@@ -127,15 +127,24 @@ __device__ __forceinline__ uint32_t nib_pair_h(uint32_t s, uint32_t m, uint32_t 
 }
 
 // The eight fp16 weights fp16(s q + b) of one packed word, in the nibble-pair
-// order (q0, q4), (q1, q5), (q2, q6), (q3, q7).
-__device__ __forceinline__ h8_t dequant_word(uint32_t w, h2_t s2, h2_t b2, uint32_t m, uint32_t c) {
+// order (q0, q4), (q1, q5), (q2, q6), (q3, q7).  Pairs 0 and 2 are the low
+// nibbles of each half of w and of w >> 8, under the exponent of 1024 (fp16
+// 1024 + q); pairs 1 and 3 are their high nibbles, left in place (bits 4-7
+// of the half) under the exponent of 64, whose mantissa step is 1/16 (fp16
+// 64 + q): one shift per word instead of three.  m_lo / c_lo = 0x000f000f /
+// 0x64006400, m_hi / c_hi = 0x00f000f0 / 0x54005400.
+__device__ __forceinline__ h8_t dequant_word(uint32_t w, h2_t s2, h2_t b2, uint32_t m_lo, uint32_t c_lo,
+                                             uint32_t m_hi, uint32_t c_hi) {
     const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const h2_t k64 = {(_Float16)64.0f, (_Float16)64.0f};
+    const uint32_t w8 = w >> 8;
+    const h2_t q[4] = {__builtin_bit_cast(h2_t, nib_pair_h(w, m_lo, c_lo)) - k1024,      // exact
+                       __builtin_bit_cast(h2_t, nib_pair_h(w, m_hi, c_hi)) - k64,
+                       __builtin_bit_cast(h2_t, nib_pair_h(w8, m_lo, c_lo)) - k1024,
+                       __builtin_bit_cast(h2_t, nib_pair_h(w8, m_hi, c_hi)) - k64};
     uint32_t out[4];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const h2_t q = __builtin_bit_cast(h2_t, nib_pair_h(w >> (4 * p), m, c)) - k1024;   // exact
-        out[p] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, b2));
-    }
+    for (int p = 0; p < 4; ++p) out[p] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q[p], s2, b2));
     return __builtin_bit_cast(h8_t, make_uint4(out[0], out[1], out[2], out[3]));
 }
 
@@ -267,9 +276,11 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
 #pragma unroll
     for (int j = 0; j < NJ; ++j) wr[j] = NMAT == 2 ? j * (BNW / 2) + wave * 32 + ccol : wave * (32 * NJ) + j * 32 + ccol;
 
-    uint32_t nib_mask, nib_exp;               // the nibble-pair constants, set up once
+    uint32_t nib_mask, nib_exp, nib_mask_hi, nib_exp_hi;   // the nibble-pair constants, set up once
     asm("s_mov_b32 %0, 0x000f000f" : "=s"(nib_mask));
     asm("v_mov_b32 %0, 0x64006400" : "=v"(nib_exp));
+    asm("s_mov_b32 %0, 0x00f000f0" : "=s"(nib_mask_hi));
+    asm("v_mov_b32 %0, 0x54005400" : "=v"(nib_exp_hi));
 
     f32x16_t acc[4][NJ];
 #pragma unroll
@@ -319,7 +330,7 @@ __global__ __launch_bounds__(kThreads, NJ == 1 ? 3 : 2) void q4_gemm16_kernel(Ge
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 const uint32_t w = ks == 0 ? bw[j].x : ks == 1 ? bw[j].y : ks == 2 ? bw[j].z : bw[j].w;
-                bo[j] = dequant_word(w, s2[j], b2[j], nib_mask, nib_exp);
+                bo[j] = dequant_word(w, s2[j], b2[j], nib_mask, nib_exp, nib_mask_hi, nib_exp_hi);
             }
         };
         auto mfmas = [&](const h8_t (&a)[4], const h8_t (&bo)[NJ]) {
